@@ -1,0 +1,294 @@
+// fq_formats.h -- device-side decoding of the five GGUF block formats.
+//
+// Every format is processed in "units" of 32 weights.  A unit is what one
+// lane decodes per step: a whole block for Q4_0/Q4_1/Q8_0, one eighth of a
+// 256-weight super-block for Q4_K/Q6_K.  A unit's 32 weights are produced in
+// a format-specific "slot" order s = 0..31 that follows the byte layout, and
+// the activation vector is staged in LDS in the same slot order, so the dot
+// product of a unit is a straight 32-term FMA chain for every format.
+//
+// The slots of a unit fall into NG equal groups that share one affine
+// coefficient pair (A_g, B_g): the unit's contribution to y is
+//      sum_g  A_g * P_g + B_g * S_g,   P_g = sum_{s in g} x_s * q_s,
+//                                      S_g = sum_{s in g} x_s,
+// with q_s the raw unsigned code of slot s.  (A, B) per format:
+//   Q4_0  (d, -8 d)            matmul.cpp:73-87     w = (q - 8) d
+//   Q4_1  (d, m)               matmul.cpp:89-104    w = q d + m
+//   Q8_0  (d, -128 d)          matmul.cpp:106-118   w = (q' - 128) d, q' = q ^ 0x80
+//   Q4_K  (d sc_g, -dmin m_g)  matmul.cpp:340-377   w = d sc q - dmin m
+//   Q6_K  (d sc_g, -32 d sc_g) matmul.cpp:242-279   w = (d sc)(q - 32)
+// S_g is computed once per staged activation vector, so the offsets cost one
+// FMA per group instead of one operation per weight.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fq {
+
+enum : int { Q4_0 = 2, Q4_1 = 3, Q4_K = 4, Q8_0 = 7, Q6_K = 13 };
+
+// ---- loads: GGUF blocks are only 2-byte aligned; gfx950 global loads accept
+// unaligned addresses, and hipcc lowers these to single dwordx{1,2,4} loads.
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+__device__ __forceinline__ uint2 ld_u64(const uint8_t* p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+
+// ---- fp16 -> fp32
+// Hardware conversion (v_cvt_f32_f16): what the reference's GEMVs use
+// (F16C _mm256_cvtph_ps, cpu_gemv.h:25-28; __half2float in CUDA).
+__device__ __forceinline__ float f16_hw(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+// The reference's scalar conversion (matmul.cpp:58-71), used by the dequant
+// path so dequantized values are bit-identical: -0 -> +0 and exponent 31
+// (Inf/NaN codes) -> (1 + m/1024) * 2^16 instead of Inf/NaN.
+__device__ __forceinline__ float f16_ref(uint32_t h) {
+    uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 31u, m = h & 0x3FFu;
+    if (e == 0) {
+        float v = (float)m * 0x1p-24f;  // exact: m < 2^10
+        return (s && m) ? -v : v;
+    }
+    return __builtin_bit_cast(float, (s << 31) | ((e + 112u) << 23) | (m << 13));
+}
+template <bool EXACT>
+__device__ __forceinline__ float f16(uint32_t h) {
+    if constexpr (EXACT) return f16_ref(h);
+    else return f16_hw(h);
+}
+
+__device__ __forceinline__ float ubyte(uint32_t w, int b) {
+    return (float)((w >> (8 * b)) & 0xFFu);
+}
+
+// Nibble unpack of 4 bytes: low nibbles to slots [lo, lo+4), high to [hi, hi+4).
+// The masks go through an opaque v_and so the compiler keeps the byte
+// extracts as v_cvt_f32_ubyte{0..3} instead of folding them into bfe + cvt.
+__device__ __forceinline__ uint32_t opaque_and(uint32_t a, uint32_t m) {
+    uint32_t r;
+    asm volatile("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(m));
+    return r;
+}
+__device__ __forceinline__ void nibbles(uint32_t w, float* q, int lo, int hi) {
+    uint32_t l = opaque_and(w, 0x0F0F0F0Fu), h = opaque_and(w >> 4, 0x0F0F0F0Fu);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        q[lo + b] = ubyte(l, b);
+        q[hi + b] = ubyte(h, b);
+    }
+}
+
+template <int F>
+struct Fmt;
+
+// ---------------------------------------------------------------- Q4_0 (18 B)
+template <>
+struct Fmt<Q4_0> {
+    static constexpr int BE = 32, BB = 18, NG = 1;
+    struct Raw {
+        uint32_t d;
+        uint4 qs;
+    };
+    __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 18 * u;
+        return Raw{ld_u16(p), ld_u128(p + 2)};
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
+        float d = f16<EXACT>(r.d);
+        nibbles(r.qs.x, q, 0, 16);
+        nibbles(r.qs.y, q, 4, 20);
+        nibbles(r.qs.z, q, 8, 24);
+        nibbles(r.qs.w, q, 12, 28);
+        A[0] = d;
+        B[0] = -8.0f * d;
+    }
+    // Bit-exact dequantized value of a slot (reference expression order).
+    __device__ static float value(float q, float A, float) { return (q - 8.0f) * A; }
+};
+
+// ---------------------------------------------------------------- Q4_1 (20 B)
+template <>
+struct Fmt<Q4_1> {
+    static constexpr int BE = 32, BB = 20, NG = 1;
+    struct Raw {
+        uint32_t dm;
+        uint4 qs;
+    };
+    __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 20 * u;
+        return Raw{ld_u32(p), ld_u128(p + 4)};
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
+        nibbles(r.qs.x, q, 0, 16);
+        nibbles(r.qs.y, q, 4, 20);
+        nibbles(r.qs.z, q, 8, 24);
+        nibbles(r.qs.w, q, 12, 28);
+        A[0] = f16<EXACT>(r.dm & 0xFFFFu);
+        B[0] = f16<EXACT>(r.dm >> 16);
+    }
+    // q*d is exact, so the fused form rounds exactly like q*d + m.
+    __device__ static float value(float q, float A, float B) { return __builtin_fmaf(q, A, B); }
+};
+
+// ---------------------------------------------------------------- Q8_0 (34 B)
+template <>
+struct Fmt<Q8_0> {
+    static constexpr int BE = 32, BB = 34, NG = 1;
+    struct Raw {
+        uint32_t d;
+        uint4 q0, q1;
+    };
+    __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 34 * u;
+        return Raw{ld_u16(p), ld_u128(p + 2), ld_u128(p + 18)};
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
+        const uint32_t v[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t b = v[i] ^ 0x80808080u;  // int8 q -> unsigned q + 128
+#pragma unroll
+            for (int j = 0; j < 4; ++j) q[4 * i + j] = ubyte(b, j);
+        }
+        float d = f16<EXACT>(r.d);
+        A[0] = d;
+        B[0] = -128.0f * d;
+    }
+    __device__ static float value(float q, float A, float) { return (q - 128.0f) * A; }
+};
+
+// --------------------------------------------------------------- Q4_K (144 B)
+// Super-block: d f16 @0, dmin f16 @2, scales[12] @4, qs[128] @16.  Unit j of
+// a super-block reads qs[16j, 16j+16): its low nibbles are elements
+// 64g + 16h + [0,16) (sub-block 2g), its high nibbles 64g + 32 + 16h + [0,16)
+// (sub-block 2g+1), g = j/2, h = j%2 (matmul.cpp:361-373).
+template <>
+struct Fmt<Q4_K> {
+    static constexpr int BE = 256, BB = 144, NG = 2;
+    struct Raw {
+        uint4 hdr;
+        uint4 qs;
+    };
+    __device__ static int k_of(int u, int s) {
+        int sb = u >> 3, j = u & 7, g = j >> 1, h = j & 1;
+        return 256 * sb + 64 * g + 16 * h + (s < 16 ? s : 16 + s);
+    }
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 144 * (u >> 3);
+        return Raw{ld_u128(p), ld_u128(p + 16 + 16 * (u & 7))};
+    }
+    // get_scale_min_k4 (matmul.cpp:232-240) for the pair (2g, 2g+1).
+    __device__ static void scale_min(const uint4& hdr, int g, uint32_t& sa, uint32_t& ma,
+                                     uint32_t& sb, uint32_t& mb) {
+        const uint32_t q0 = hdr.y, q4 = hdr.z, q8 = hdr.w;  // scales bytes 0-3, 4-7, 8-11
+        if (g < 2) {
+            int sh = 16 * g;  // byte 2g
+            sa = (q0 >> sh) & 63u;
+            ma = (q4 >> sh) & 63u;
+            sb = (q0 >> (sh + 8)) & 63u;
+            mb = (q4 >> (sh + 8)) & 63u;
+        } else {
+            int sh = 16 * (g - 2);  // byte index is-4 = 2g-4
+            uint32_t a8 = q8 >> sh, a0 = q0 >> sh, a4 = q4 >> sh;
+            sa = (a8 & 0xFu) | (((a0 >> 6) & 3u) << 4);
+            ma = ((a8 >> 4) & 0xFu) | (((a4 >> 6) & 3u) << 4);
+            sb = ((a8 >> 8) & 0xFu) | (((a0 >> 14) & 3u) << 4);
+            mb = ((a8 >> 12) & 0xFu) | (((a4 >> 14) & 3u) << 4);
+        }
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int u, float* q, float* A, float* B) {
+        nibbles(r.qs.x, q, 0, 16);
+        nibbles(r.qs.y, q, 4, 20);
+        nibbles(r.qs.z, q, 8, 24);
+        nibbles(r.qs.w, q, 12, 28);
+        float d = f16<EXACT>(r.hdr.x & 0xFFFFu), dmin = f16<EXACT>(r.hdr.x >> 16);
+        uint32_t sa, ma, sb, mb;
+        scale_min(r.hdr, (u & 7) >> 1, sa, ma, sb, mb);
+        A[0] = d * (float)sa;
+        B[0] = -(dmin * (float)ma);
+        A[1] = d * (float)sb;
+        B[1] = -(dmin * (float)mb);
+    }
+    // (d*sc)*q is exact, so fma(A, q, -dmin*m) rounds like d1*q - m1.
+    __device__ static float value(float q, float A, float B) { return __builtin_fmaf(A, q, B); }
+};
+
+// --------------------------------------------------------------- Q6_K (210 B)
+// Super-block: ql[128] @0, qh[64] @128, sc int8[16] @192, d f16 @208.  Unit
+// j = 4n + c covers l in [8c, 8c+8) of half n: slot 8g + e holds element
+// 128n + 32g + 8c + e, g = 0..3 (matmul.cpp:259-276).
+template <>
+struct Fmt<Q6_K> {
+    static constexpr int BE = 256, BB = 210, NG = 4;
+    struct Raw {
+        uint2 ql_lo, ql_hi, qh, sc;
+        uint32_t d;
+    };
+    __device__ static int k_of(int u, int s) {
+        int sb = u >> 3, j = u & 7, n = j >> 2, c = j & 3;
+        return 256 * sb + 128 * n + 32 * (s >> 3) + 8 * c + (s & 7);
+    }
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 210 * (u >> 3);
+        int j = u & 7, n = j >> 2, l0 = 8 * (j & 3);
+        return Raw{ld_u64(p + 64 * n + l0), ld_u64(p + 64 * n + 32 + l0),
+                   ld_u64(p + 128 + 32 * n + l0), ld_u64(p + 192 + 8 * n), ld_u16(p + 208)};
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int u, float* q, float* A, float* B) {
+        const uint32_t a[2] = {r.ql_lo.x, r.ql_lo.y}, b[2] = {r.ql_hi.x, r.ql_hi.y},
+                       h[2] = {r.qh.x, r.qh.y};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint32_t q1 = (a[i] & 0x0F0F0F0Fu) | ((h[i] & 0x03030303u) << 4);
+            uint32_t q2 = (b[i] & 0x0F0F0F0Fu) | ((h[i] & 0x0C0C0C0Cu) << 2);
+            uint32_t q3 = ((a[i] >> 4) & 0x0F0F0F0Fu) | (h[i] & 0x30303030u);
+            uint32_t q4 = ((b[i] >> 4) & 0x0F0F0F0Fu) | ((h[i] >> 2) & 0x30303030u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                q[0 + 4 * i + e] = ubyte(q1, e);
+                q[8 + 4 * i + e] = ubyte(q2, e);
+                q[16 + 4 * i + e] = ubyte(q3, e);
+                q[24 + 4 * i + e] = ubyte(q4, e);
+            }
+        }
+        float d = f16<EXACT>(r.d);
+        int is = (u & 3) >> 1;  // l/16 for l in [8c, 8c+8)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            int t = is + 2 * g;  // sc[8n + is + 2g]
+            uint32_t word = t < 4 ? r.sc.x : r.sc.y;
+            int sc = (int)(int8_t)((word >> (8 * (t & 3))) & 0xFFu);
+            A[g] = d * (float)sc;
+            B[g] = -32.0f * A[g];
+        }
+    }
+    // (d*sc) exact; one rounding of (d*sc)*(q-32), as the reference.
+    __device__ static float value(float q, float A, float) { return A * (q - 32.0f); }
+};
+
+}  // namespace fq

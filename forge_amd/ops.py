@@ -1,0 +1,110 @@
+"""Operator-level mirror of Forge's quantized matmul API on the HIP device.
+
+``matmul_transB(a, b, bias)`` follows ``forge::ops::matmul_transB``
+(include/forge/operator_matmul.h:9, src/operators/cpu/matmul.cpp:1134-1286):
+same argument meaning (a: fp32 [M, K]; b: block-quantized weight of logical
+shape [N, K]; optional bias [N] or [M, N]), same dispatch on M, a new fp32
+[M, N] output, and the reference's error messages for the conditions it
+rejects.  torch only provides device memory and the current stream here; all
+arithmetic runs in libforge_q.so through the C ABI.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .formats import fmt
+
+
+@dataclass
+class QWeight:
+    """A block-quantized weight: raw GGUF block bytes on the device.
+
+    Mirrors a forge::Tensor whose dtype is a block format and whose shape is
+    [N, K] in elements (include/forge/tensor.h:11-68); ``data`` holds
+    N * row_bytes(K) bytes, rows contiguous.
+    """
+    data: torch.Tensor  # uint8, contiguous, on the device
+    dtype: int
+    N: int
+    K: int
+
+    @property
+    def shape(self):
+        return (self.N, self.K)
+
+    def ndim(self) -> int:
+        return 2
+
+    @classmethod
+    def from_numpy(cls, blocks, dtype: int, N: int, K: int, device="cuda"):
+        t = torch.from_numpy(blocks.reshape(-1)).to(device)
+        return cls(t, int(dtype), int(N), int(K))
+
+
+def _stream_ptr(t: torch.Tensor):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def matmul_transB(a: torch.Tensor, b: QWeight, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """out[M, N] = a[M, K] @ dequant(b)[N, K]^T (+ bias), on the device."""
+    if a.dim() != 2 or b.ndim() != 2:
+        raise RuntimeError("matmul_transB expects 2D tensors")
+    M, K = a.shape
+    if K != b.K:
+        raise RuntimeError(f"matmul_transB dimension mismatch: K={K} K2={b.K} "
+                           f"b_shape=[{b.N},{b.K}]")
+    if a.dtype != torch.float32 or not a.is_cuda or not a.is_contiguous():
+        raise RuntimeError("matmul_transB: input must be a contiguous fp32 device tensor")
+    out = torch.empty((M, b.N), dtype=torch.float32, device=a.device)
+    bias_ptr, bias_ndim, bias_len = None, 0, 0
+    if bias is not None:
+        bias = bias.to(device=a.device, dtype=torch.float32).contiguous()
+        bias_ptr, bias_ndim, bias_len = bias.data_ptr(), bias.dim(), bias.numel()
+    st = _lib.lib().fq_matmul_transB(b.dtype, a.data_ptr(), b.data.data_ptr(), bias_ptr,
+                                     bias_ndim, bias_len, out.data_ptr(), M, K, b.N,
+                                     _stream_ptr(a))
+    if st == _lib.FQ_ERR_DTYPE:
+        raise RuntimeError("Unsupported quantized type in matmul_transB CUDA")
+    _lib.check(st, "matmul_transB")
+    return out
+
+
+def gemv(x: torch.Tensor, b: QWeight) -> torch.Tensor:
+    """Batch-1 GEMV through fq_gemv (x: [K] or [1, K])."""
+    xv = x.reshape(-1)
+    y = torch.empty((b.N,), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_gemv(b.dtype, xv.data_ptr(), b.data.data_ptr(), y.data_ptr(),
+                                  b.K, b.N, _stream_ptr(x)), "fq_gemv")
+    return y
+
+
+def gemv_batch(x: torch.Tensor, b: QWeight) -> torch.Tensor:
+    M = x.shape[0]
+    y = torch.empty((M, b.N), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_gemv_batch(b.dtype, x.data_ptr(), b.data.data_ptr(), y.data_ptr(),
+                                        M, b.K, b.N, _stream_ptr(x)), "fq_gemv_batch")
+    return y
+
+
+def matmul_prefill(x: torch.Tensor, b: QWeight) -> torch.Tensor:
+    M = x.shape[0]
+    y = torch.empty((M, b.N), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_matmul_prefill(b.dtype, x.data_ptr(), b.data.data_ptr(),
+                                            y.data_ptr(), M, b.K, b.N, _stream_ptr(x)),
+               "fq_matmul_prefill")
+    return y
+
+
+def dequantize_weight(b: QWeight) -> torch.Tensor:
+    """fp32 [N, K] dequantized copy, bit-identical to the reference's rows."""
+    out = torch.empty((b.N, b.K), dtype=torch.float32, device=b.data.device)
+    _lib.check(_lib.lib().fq_dequant_rows(b.dtype, b.data.data_ptr(), out.data_ptr(), b.N, b.K,
+                                          _stream_ptr(b.data)), "fq_dequant_rows")
+    return out
+
+
+def row_bytes(dtype: int, K: int) -> int:
+    return fmt(dtype).row_bytes(K)

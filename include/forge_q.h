@@ -1,0 +1,109 @@
+/*
+ * forge_q.h -- C ABI of the MI355X (gfx950) quantized-matmul hot path.
+ *
+ * This is the seam Forge's operator layer calls into on the GPU device.  It
+ * replaces the CUDA function-pointer tables and launchers the reference
+ * binds today; every entry point cites the reference interface it replaces.
+ * Plain pointers, sizes and an opaque stream handle only: no C++ or torch
+ * types cross this boundary, and nothing throws across it.
+ *
+ * Conventions (shared by all entry points)
+ *  - dtype: a forge::DataType value (include/forge/types.h:7-26 of the
+ *    reference): Q4_0=2, Q4_1=3, Q4_K=4, Q8_0=7, Q6_K=13.
+ *  - w: device pointer to a row-major [N][K/block_elems] array of on-disk
+ *    GGUF blocks, rows contiguous with no padding (the layout
+ *    forge::compute_quantized_bytes sizes, quant_traits.h:138-146).  No
+ *    alignment beyond 2 bytes is required.
+ *  - x: device fp32 [M][K] row-major; y: device fp32 [M][N] row-major.
+ *  - stream: a hipStream_t passed as void*; NULL is the null stream.  All
+ *    entry points are asynchronous with respect to the host, like the
+ *    reference's launchers (cuda_gemv_tmpl.cuh:332-351).
+ *  - K must be a multiple of the format's block size for the matmul entry
+ *    points (GGUF guarantees this for every weight tensor).
+ *  - Return value: FQ_OK or one of the FQ_ERR_* codes below; the reference
+ *    throws std::runtime_error for the same conditions (matmul.cpp:1135-1146,
+ *    1163-1165, 1315) or launches unchecked.
+ *  - Calls that need a split-K partial buffer use a library-owned per-device,
+ *    per-stream workspace that grows on demand and lives until the process
+ *    ends; concurrent calls on one stream are ordered by the stream.
+ */
+#ifndef FORGE_Q_H
+#define FORGE_Q_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FQ_OK 0
+#define FQ_ERR_DTYPE 1    /* dtype is not one of the five block formats          */
+#define FQ_ERR_SHAPE 2    /* M/N/K out of range or K not a multiple of the block  */
+#define FQ_ERR_NULL 3     /* a required pointer is NULL                           */
+#define FQ_ERR_HIP 4      /* the HIP runtime reported an error (fq_last_hip_error) */
+#define FQ_ERR_NO_DEVICE 5
+
+/* DataType values accepted by the entry points. */
+#define FQ_DTYPE_Q4_0 2u
+#define FQ_DTYPE_Q4_1 3u
+#define FQ_DTYPE_Q4_K 4u
+#define FQ_DTYPE_Q8_0 7u
+#define FQ_DTYPE_Q6_K 13u
+
+/* Block geometry of a dtype: elements and bytes per block.
+ * Replaces data_type_traits[] lookups (src/operators/cpu/quant_traits.cpp:33-52,
+ * dtype_block_elements / dtype_block_size, quant_traits.h:118-124). */
+int fq_block_info(uint32_t dtype, int* block_elems, int* block_bytes);
+
+/* Human-readable text for a status code (static storage). */
+const char* fq_status_str(int status);
+
+/* The hipError_t value behind the most recent FQ_ERR_HIP on this thread. */
+int fq_last_hip_error(void);
+
+/* Batch-1 fused dequant+GEMV: y[n] = sum_k x[k] * dequant(w)[n][k].
+ * Replaces cuda::gemv_dispatch[dtype](x, w, y, K, N, stream)
+ * (src/operators/cuda/cuda_gemv.h:29-33, table cuda_gemv_instances.cu:36-76,
+ * called from matmul.cpp:1246-1249) and the Q4_0 special launcher
+ * launch_gemv_q4_0_transB (cuda_gemv.cu:183-208). */
+int fq_gemv(uint32_t dtype, const float* x, const void* w, float* y, int K, int N, void* stream);
+
+/* Small-batch fused dequant+matmul, 1 <= M <= 32: y[m][n] = x[m] . W[n].
+ * Replaces cuda::gemv_batch_dispatch[dtype](x, w, y, M, K, N, stream)
+ * (cuda_gemv.h:29-33, called from matmul.cpp:1156-1161).  Activations stay
+ * fp32 and are not quantized, as in the reference. */
+int fq_gemv_batch(uint32_t dtype, const float* x, const void* w, float* y, int M, int K, int N,
+                  void* stream);
+
+/* Prefill matmul for M > 32 (dense contraction on MFMA).
+ * Replaces the reference's dequantize-to-fp32 + cublasGemmEx pair
+ * (launch_dequant_*_matrix + launch_cublas_sgemm, matmul.cpp:1190-1243,
+ * cuda_quant.cu:582-598) and its Q8_0 host round-trip (matmul.cpp:1216-1238). */
+int fq_matmul_prefill(uint32_t dtype, const float* x, const void* w, float* y, int M, int K,
+                      int N, void* stream);
+
+/* Device branch of ops::matmul_transB (matmul.cpp:1134-1286) for block
+ * weights: dispatches on M exactly as the reference does (M == 1 -> GEMV,
+ * 1 < M <= 32 -> small batch, M > 32 -> prefill) and applies the optional
+ * bias like apply_bias (matmul.cpp:1005-1049):
+ *   bias_ndim == 1: y[m][n] += bias[n] for n < min(bias_len, N)
+ *   bias_ndim == 2: y[i]    += bias[i] for i < M*N (bias_len must be >= M*N)
+ *   bias == NULL or bias_ndim == 0: no bias.
+ * bias must be a device pointer. */
+int fq_matmul_transB(uint32_t dtype, const float* x, const void* w, const float* bias,
+                     int bias_ndim, int64_t bias_len, float* y, int M, int K, int N,
+                     void* stream);
+
+/* Dequantize rows [0, N) of w into out[N][K] fp32, bit-identical to the
+ * reference's dequantize_*_row (matmul.cpp:73-377), including its scalar
+ * fp16 conversion (fp16 Inf/NaN scale codes map to finite values, -0 to +0).
+ * K need not be a multiple of the block.  Replaces launch_dequant_*_matrix
+ * (cuda_quant.cu:131-335) and backs ops::dequantize_weight
+ * (matmul.cpp:980-1003). */
+int fq_dequant_rows(uint32_t dtype, const void* w, float* out, int N, int K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FORGE_Q_H */

@@ -1,0 +1,134 @@
+"""Write the golden vectors for the quantized-matmul hot path.
+
+Runs the reference's OWN compiled CPU code (oracle/_ref/libforge_ref.so, built
+by ``make -C oracle ref`` from the reference sources in place) on seeded
+inputs and stores inputs and outputs as small .npz fixtures beside this
+script.  The fixtures are data: block bytes, activations, the reference's
+dequantized rows and the reference's ops::matmul_transB outputs.
+
+Usage:  python tests/golden/gen_golden.py
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from forge_amd import formats as F  # noqa: E402
+from forge_amd import synth  # noqa: E402
+
+P = ctypes.c_void_p
+
+# fp16 bit patterns for scale fields in the edge cases: +-0, smallest and
+# largest subnormal, smallest normal, 1.0, largest finite, and the Inf/NaN
+# codes the reference's scalar converter maps to finite values.
+SPECIAL_F16 = [0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0xFBFF,
+               0x8001, 0xBC00, 0x7C00, 0xFC00, 0x7E00]
+FINITE_F16 = [h for h in SPECIAL_F16 if (h & 0x7C00) != 0x7C00]
+
+SCALE_OFFSETS = {  # byte offsets of fp16 fields inside a block
+    F.Q4_0: [0], F.Q4_1: [0, 2], F.Q8_0: [0], F.Q4_K: [0, 2], F.Q6_K: [208],
+}
+
+
+def lib():
+    path = os.path.join(ROOT, "oracle", "_ref", "libforge_ref.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} missing: run `make -C oracle ref` first")
+    return ctypes.CDLL(path)
+
+
+def ref_dequant(L, dt, w, N, K):
+    out = np.zeros((N, K), np.float32)
+    assert L.fqr_dequant_rows(dt, w.ctypes.data_as(P), out.ctypes.data_as(P), N, K) == 0
+    return out
+
+
+def ref_matmul(L, dt, x, w, M, K, N):
+    y = np.zeros((M, N), np.float32)
+    rc = L.fqr_matmul_transB(dt, x.ctypes.data_as(P), w.ctypes.data_as(P),
+                             y.ctypes.data_as(P), M, K, N, 4)
+    assert rc == 0, rc
+    return y
+
+
+def set_scales(w, f, K, patterns):
+    nb = -(-K // f.block_elems)
+    blk = w.reshape(w.shape[0], nb, f.block_bytes)
+    i = 0
+    for n in range(blk.shape[0]):
+        for b in range(nb):
+            for off in SCALE_OFFSETS[f.dtype]:
+                h = patterns[i % len(patterns)]
+                blk[n, b, off] = h & 0xFF
+                blk[n, b, off + 1] = h >> 8
+                i += 1
+
+
+def extreme_payload(w, f, K):
+    """Saturate the quant payload of every other row (all-0 / all-1 bits)."""
+    nb = -(-K // f.block_elems)
+    blk = w.reshape(w.shape[0], nb, f.block_bytes)
+    lo = {F.Q4_0: 2, F.Q4_1: 4, F.Q8_0: 2, F.Q4_K: 4, F.Q6_K: 0}[f.dtype]
+    hi = {F.Q4_0: 18, F.Q4_1: 20, F.Q8_0: 34, F.Q4_K: 144, F.Q6_K: 208}[f.dtype]
+    blk[0::4, :, lo:hi] = 0x00
+    blk[1::4, :, lo:hi] = 0xFF
+    if f.dtype == F.Q8_0:
+        blk[2::4, :, lo:hi] = 0x80  # int8 -128, outside the synthetic range
+        blk[3::4, :, lo:hi] = 0x7F
+
+
+def main():
+    L = lib()
+    for dt, f in F.FORMATS.items():
+        cases = {}
+        K = 512 if f.block_elems == 32 else 1024
+        N = 7  # not a multiple of the reference's 4-row decode tile
+        w = synth.make_weights(dt, N, K, seed=100 + dt)
+        x1 = synth.make_x(1, K, seed=200 + dt)
+        x3 = synth.make_x(3, K, seed=300 + dt)
+        cases["rand"] = dict(w=w, K=K, x1=x1, x3=x3)
+
+        we = synth.make_weights(dt, 8, K, seed=400 + dt)
+        extreme_payload(we, f, K)
+        set_scales(we, f, K, FINITE_F16)
+        cases["edge"] = dict(w=we, K=K, x1=synth.make_x(1, K, seed=500 + dt),
+                             x3=synth.make_x(3, K, seed=600 + dt))
+
+        wi = synth.make_weights(dt, 4, K, seed=700 + dt)
+        set_scales(wi, f, K, SPECIAL_F16)
+        cases["specialf16"] = dict(w=wi, K=K)  # dequant only (Inf/NaN codes)
+
+        # Ragged K (not a multiple of the block): dequant only.
+        Kr = 80 if f.block_elems == 32 else 300
+        nbr = -(-Kr // f.block_elems)
+        rng = np.random.default_rng(800 + dt)
+        wr = rng.integers(0, 256, size=(5, nbr * f.block_bytes), dtype=np.uint8)
+        set_scales(wr, f, Kr, FINITE_F16)
+        cases["ragged"] = dict(w=wr, K=Kr)
+
+        out = {}
+        for name, c in cases.items():
+            w, K = c["w"], c["K"]
+            N = w.shape[0]
+            out[f"{name}/w"] = w
+            out[f"{name}/K"] = np.int64(K)
+            out[f"{name}/deq"] = ref_dequant(L, dt, w, N, K)
+            for xk in ("x1", "x3"):
+                if xk in c:
+                    x = c[xk]
+                    out[f"{name}/{xk}"] = x
+                    out[f"{name}/y_{xk}"] = ref_matmul(L, dt, x, w, x.shape[0], K, N)
+        path = os.path.join(HERE, f"golden_{f.name}.npz")
+        np.savez_compressed(path, dtype=np.int64(dt), **out)
+        print(f"wrote {path} ({os.path.getsize(path)} B)")
+
+
+if __name__ == "__main__":
+    main()
