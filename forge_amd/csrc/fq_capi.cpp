@@ -7,6 +7,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
+#include <cstdlib>
+#include <cstdint>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -60,62 +63,90 @@ DevInfo device_info(int dev) {
     return d;
 }
 
-// Split-K partial buffers: one grow-only buffer per (device, stream), kept
-// until process exit, so calls on different streams never share one.
-float* workspace(int dev, hipStream_t st, size_t bytes, hipError_t& err) {
+// Split-K workspace: one grow-only pair of buffers per (device, stream) --
+// partial sums and arrival counters -- kept until process exit, so calls on
+// different streams never share one.  Counters are zeroed when allocated and
+// every call leaves them zero again.
+struct Workspace {
+    float* part = nullptr;
+    size_t part_bytes = 0;
+    unsigned* cnt = nullptr;
+    size_t cnt_words = 0;
+};
+
+hipError_t workspace(int dev, hipStream_t st, size_t part_bytes, size_t cnt_words, int grid,
+                     float** part, unsigned** cnt) {
     static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
+    static std::map<std::pair<int, hipStream_t>, Workspace> bufs;
     std::lock_guard<std::mutex> lk(mu);
-    auto& b = bufs[{dev, st}];
-    err = hipSuccess;
-    if (b.second < bytes) {
-        if (b.first) {
-            // the old buffer may still be read by queued work on this stream
+    Workspace& w = bufs[{dev, st}];
+    hipError_t err = hipSuccess;
+    if (w.part_bytes < part_bytes || w.cnt_words < cnt_words) {
+        // the old buffers may still be in use by queued work on this stream
+        if (w.part || w.cnt) {
             err = hipStreamSynchronize(st);
-            if (err != hipSuccess) return nullptr;
-            hipFree(b.first);
-            b = {nullptr, 0};
+            if (err != hipSuccess) return err;
         }
-        err = hipMalloc(&b.first, bytes);
-        if (err != hipSuccess) {
-            b = {nullptr, 0};
-            return nullptr;
+        if (w.part_bytes < part_bytes) {
+            if (w.part) hipFree(w.part);
+            w.part = nullptr;
+            w.part_bytes = 0;
+            err = hipMalloc(reinterpret_cast<void**>(&w.part), part_bytes);
+            if (err != hipSuccess) return err;
+            w.part_bytes = part_bytes;
         }
-        b.second = bytes;
+        if (w.cnt_words < cnt_words) {
+            if (w.cnt) hipFree(w.cnt);
+            w.cnt = nullptr;
+            w.cnt_words = 0;
+            err = hipMalloc(reinterpret_cast<void**>(&w.cnt), cnt_words * sizeof(unsigned));
+            if (err != hipSuccess) return err;
+            w.cnt_words = cnt_words;
+            err = fq::launch_zero(w.cnt, cnt_words, grid, st);
+            if (err != hipSuccess) return err;
+        }
     }
-    return static_cast<float*>(b.first);
+    *part = w.part;
+    *cnt = w.cnt;
+    return hipSuccess;
 }
 
 constexpr int kWG = 256;
 constexpr int kT = 16;
+constexpr int kRowsPerWG = 16;
+constexpr int kMaxNU = 8;
 
-// Plan a launch of gemv_kernel for M tokens processed MT at a time.
+// Plan a launch of gemv_kernel for M tokens processed MT at a time: as few
+// K-splits as keep every lane at <= 8 units per row (more only when there are
+// fewer row groups than CUs), then enough persistent work-groups to fill the
+// chip once.
 int plan(uint32_t dtype, const Geometry& g, int M, int K, int N, int MT, const DevInfo& di,
          fq::LaunchCfg& c, int& U, int& Uc) {
+    (void)g;
     U = K / 32;
-    const int rows_per_wg = (kWG / 64) * (64 / kT);
-    const long RG = (N + rows_per_wg - 1) / rows_per_wg;
+    const long RG = (N + kRowsPerWG - 1) / kRowsPerWG;
     const int TG = (M + MT - 1) / MT;
-    const long target = 2L * di.cus;
-    int S = 1;
-    while (RG * S * TG < target && U / (2 * S) >= 2 * kT) S *= 2;
+    int S = std::max(1, (U + kMaxNU * kT - 1) / (kMaxNU * kT));
+    while (RG * S * TG < di.cus && (U + S) / (S + 1) >= 2 * kT) ++S;
     auto lds_of = [&](int uc) { return (size_t)MT * uc * 36 * sizeof(float); };
     const size_t lds_cap = std::min<size_t>(di.lds, 160 * 1024);
     while (lds_of((U + S - 1) / S) > lds_cap) ++S;
-    Uc = (U + S - 1) / S;
-    S = (U + Uc - 1) / Uc;
+    Uc = U > 0 ? (U + S - 1) / S : 0;
+    S = U > 0 ? (U + Uc - 1) / Uc : 1;
+    const int nu = (Uc + kT - 1) / kT;
     c.T = kT;
     c.MT = MT;
+    c.NU = nu <= 2 ? 2 : nu <= 4 ? 4 : 8;
     c.splits = S;
     c.token_groups = TG;
     c.lds_bytes = lds_of(Uc);
-    int per_cu = 0;
-    const void* fn = fq::gemv_kernel_fn((int)dtype, kT, MT);
+    const void* fn = fq::gemv_kernel_fn((int)dtype, kT, MT, c.NU);
     if (!fn) return FQ_ERR_DTYPE;
+    int per_cu = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWG, c.lds_bytes);
     if (e != hipSuccess) return hip_fail(e);
     if (per_cu < 1) per_cu = 1;
-    long gx = (long)di.cus * per_cu / ((long)S * TG);
+    const long gx = (long)di.cus * per_cu / ((long)S * TG);
     c.grid_x = (int)std::max(1L, std::min(RG, gx));
     return FQ_OK;
 }
@@ -127,17 +158,69 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     if (M < 0 || N < 0 || K < 0) return FQ_ERR_SHAPE;
     if (K % g.be != 0) return FQ_ERR_SHAPE;
     if (M == 0 || N == 0) return FQ_OK;
-    if (K == 0) {
-        hipError_t e = hipMemsetAsync(y, 0, sizeof(float) * (size_t)M * N, st);
-        return e == hipSuccess ? FQ_OK : hip_fail(e);
-    }
     if (!x || !w || !y) return FQ_ERR_NULL;
     if (bias_mode != 0 && !bias) return FQ_ERR_NULL;
     if (bias_mode == 2 && bias_len < (int64_t)M * N) return FQ_ERR_SHAPE;
+    if ((int64_t)(K / g.be) * g.bb > INT32_MAX) return FQ_ERR_SHAPE;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e);
     const DevInfo di = device_info(dev);
+    if (K == 0 && bias_mode == 0) {
+        // a zero-length contraction: y = 0 (with a bias the kernel writes y = bias)
+        e = fq::launch_zero(reinterpret_cast<uint32_t*>(y), (size_t)M * N, di.cus, st);
+        return e == hipSuccess ? FQ_OK : hip_fail(e);
+    }
+
+    if (M == 1 && K > 0) {
+        // batch 1: persistent work-groups, as many as fit on every CU
+        const int U1 = K / 32;
+        static const int wg_env = [] {
+            const char* v = getenv("FQ_GEMV1_WG");
+            return v ? atoi(v) : 1024;
+        }();
+        int wg = wg_env;
+        size_t lds = fq::gemv1_lds_bytes((int)dtype, U1, wg);
+        const void* fn = fq::gemv1_kernel_fn((int)dtype, bias_mode != 0, wg);
+        static const bool no_rowstep = getenv("FQ_NO_ROWSTEP") != nullptr;
+        int npr = 0;
+        size_t lds_r = 0;
+        int wg_r = 0;
+        const void* fr = no_rowstep ? nullptr
+                                    : fq::gemv1r_kernel_fn((int)dtype, U1, (K / g.be) * g.bb,
+                                                           bias_mode != 0, &npr, &lds_r, &wg_r);
+        if (fr && lds_r <= std::min<size_t>(di.lds, 160 * 1024)) {
+            fn = fr;
+            lds = lds_r;
+            wg = wg_r;
+        }
+        if (fn && lds <= std::min<size_t>(di.lds, 160 * 1024)) {
+            int per_cu = 0;
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wg, lds);
+            if (e != hipSuccess) return hip_fail(e);
+            if (per_cu >= 1) {
+                fq::GemvArgs a{};
+                a.x = x;
+                a.w = static_cast<const uint8_t*>(w);
+                a.y = y;
+                a.bias = bias;
+                a.bias_len = bias_mode == 0 ? 0 : bias_len;
+                a.bias_mode = bias_mode;
+                a.M = 1;
+                a.K = K;
+                a.N = N;
+                a.U = U1;
+                a.Uc = U1;
+                a.row_bytes = (K / g.be) * g.bb;
+                const int wpb = wg / 64;
+                const long waves = (long)di.cus * per_cu * wpb;
+                const long need = std::min<long>(waves, N);
+                const int grid = (int)std::max(1L, (need + wpb - 1) / wpb);
+                e = fq::launch_raw(fn, a, grid, wg, lds, st);
+                return e == hipSuccess ? FQ_OK : hip_fail(e);
+            }
+        }
+    }
 
     fq::LaunchCfg c{};
     int U = 0, Uc = 0;
@@ -155,21 +238,18 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     a.K = K;
     a.N = N;
     a.U = U;
-    a.Uc = Uc;
+    a.Uc = std::max(Uc, 1);
     a.row_bytes = (K / g.be) * g.bb;
+    a.rg_total = (N + kRowsPerWG - 1) / kRowsPerWG;
     a.part = nullptr;
+    a.counters = nullptr;
     if (c.splits > 1) {
-        a.part = workspace(dev, st, sizeof(float) * (size_t)c.splits * M * N, e);
-        if (!a.part) return hip_fail(e);
+        e = workspace(dev, st, sizeof(float) * (size_t)c.splits * M * N,
+                      (size_t)c.token_groups * a.rg_total, di.cus, &a.part, &a.counters);
+        if (e != hipSuccess) return hip_fail(e);
     }
     e = fq::launch_gemv((int)dtype, a, c, st);
     if (e != hipSuccess) return hip_fail(e);
-    if (c.splits > 1) {
-        size_t MN = (size_t)M * N;
-        int grid = (int)std::min<size_t>((MN + 255) / 256, (size_t)di.cus * 8);
-        e = fq::launch_finalize(a.part, y, c.splits, M, N, bias, bias_mode, bias_len, grid, st);
-        if (e != hipSuccess) return hip_fail(e);
-    }
     return FQ_OK;
 }
 

@@ -30,25 +30,67 @@ enum : int { Q4_0 = 2, Q4_1 = 3, Q4_K = 4, Q8_0 = 7, Q6_K = 13 };
 
 // ---- loads: GGUF blocks are only 2-byte aligned; gfx950 global loads accept
 // unaligned addresses, and hipcc lowers these to single dwordx{1,2,4} loads.
+// The NT variants set the non-temporal hint: weights are streamed exactly
+// once per call, so they should not displace the activations in the caches.
+typedef uint32_t fq_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t fq_u32x4 __attribute__((ext_vector_type(4)));
+
+#if defined(FQ_PROBE_ALIGNED)
+#define FQ_ALIGN_PROBE(p) ((p) - (reinterpret_cast<uintptr_t>(p) & 15))
+#else
+#define FQ_ALIGN_PROBE(p) (p)
+#endif
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    p = FQ_ALIGN_PROBE(p);
     uint16_t v;
     __builtin_memcpy(&v, p, 2);
     return v;
 }
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
+    p = FQ_ALIGN_PROBE(p);
     uint32_t v;
     __builtin_memcpy(&v, p, 4);
     return v;
 }
 __device__ __forceinline__ uint2 ld_u64(const uint8_t* p) {
+    p = FQ_ALIGN_PROBE(p);
     uint2 v;
     __builtin_memcpy(&v, p, 8);
     return v;
 }
 __device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
+    p = FQ_ALIGN_PROBE(p);
     uint4 v;
     __builtin_memcpy(&v, p, 16);
     return v;
+}
+template <bool NT>
+__device__ __forceinline__ uint32_t ldg16(const uint8_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+    else return ld_u16(p);
+}
+template <bool NT>
+__device__ __forceinline__ uint32_t ldg32(const uint8_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    else return ld_u32(p);
+}
+template <bool NT>
+__device__ __forceinline__ uint2 ldg64(const uint8_t* p) {
+    if constexpr (NT) {
+        fq_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const fq_u32x2*>(p));
+        return make_uint2(v.x, v.y);
+    } else {
+        return ld_u64(p);
+    }
+}
+template <bool NT>
+__device__ __forceinline__ uint4 ldg128(const uint8_t* p) {
+    if constexpr (NT) {
+        fq_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const fq_u32x4*>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return ld_u128(p);
+    }
 }
 
 // ---- fp16 -> fp32
@@ -107,9 +149,10 @@ struct Fmt<Q4_0> {
         uint4 qs;
     };
     __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    template <bool NT = false>
     __device__ static Raw load(const uint8_t* row, int u) {
         const uint8_t* p = row + 18 * u;
-        return Raw{ld_u16(p), ld_u128(p + 2)};
+        return Raw{ldg16<NT>(p), ldg128<NT>(p + 2)};
     }
     template <bool EXACT>
     __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
@@ -134,9 +177,10 @@ struct Fmt<Q4_1> {
         uint4 qs;
     };
     __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    template <bool NT = false>
     __device__ static Raw load(const uint8_t* row, int u) {
         const uint8_t* p = row + 20 * u;
-        return Raw{ld_u32(p), ld_u128(p + 4)};
+        return Raw{ldg32<NT>(p), ldg128<NT>(p + 4)};
     }
     template <bool EXACT>
     __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
@@ -160,9 +204,10 @@ struct Fmt<Q8_0> {
         uint4 q0, q1;
     };
     __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    template <bool NT = false>
     __device__ static Raw load(const uint8_t* row, int u) {
         const uint8_t* p = row + 34 * u;
-        return Raw{ld_u16(p), ld_u128(p + 2), ld_u128(p + 18)};
+        return Raw{ldg16<NT>(p), ldg128<NT>(p + 2), ldg128<NT>(p + 18)};
     }
     template <bool EXACT>
     __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
@@ -196,9 +241,10 @@ struct Fmt<Q4_K> {
         int sb = u >> 3, j = u & 7, g = j >> 1, h = j & 1;
         return 256 * sb + 64 * g + 16 * h + (s < 16 ? s : 16 + s);
     }
+    template <bool NT = false>
     __device__ static Raw load(const uint8_t* row, int u) {
         const uint8_t* p = row + 144 * (u >> 3);
-        return Raw{ld_u128(p), ld_u128(p + 16 + 16 * (u & 7))};
+        return Raw{ldg128<NT>(p), ldg128<NT>(p + 16 + 16 * (u & 7))};
     }
     // get_scale_min_k4 (matmul.cpp:232-240) for the pair (2g, 2g+1).
     __device__ static void scale_min(const uint4& hdr, int g, uint32_t& sa, uint32_t& ma,
@@ -252,11 +298,13 @@ struct Fmt<Q6_K> {
         int sb = u >> 3, j = u & 7, n = j >> 2, c = j & 3;
         return 256 * sb + 128 * n + 32 * (s >> 3) + 8 * c + (s & 7);
     }
+    template <bool NT = false>
     __device__ static Raw load(const uint8_t* row, int u) {
         const uint8_t* p = row + 210 * (u >> 3);
         int j = u & 7, n = j >> 2, l0 = 8 * (j & 3);
-        return Raw{ld_u64(p + 64 * n + l0), ld_u64(p + 64 * n + 32 + l0),
-                   ld_u64(p + 128 + 32 * n + l0), ld_u64(p + 192 + 8 * n), ld_u16(p + 208)};
+        return Raw{ldg64<NT>(p + 64 * n + l0), ldg64<NT>(p + 64 * n + 32 + l0),
+                   ldg64<NT>(p + 128 + 32 * n + l0), ldg64<NT>(p + 192 + 8 * n),
+                   ldg16<NT>(p + 208)};
     }
     template <bool EXACT>
     __device__ static void decode(const Raw& r, int u, float* q, float* A, float* B) {
@@ -290,5 +338,130 @@ struct Fmt<Q6_K> {
     // (d*sc) exact; one rounding of (d*sc)*(q-32), as the reference.
     __device__ static float value(float q, float A, float) { return A * (q - 32.0f); }
 };
+
+// ---------------------------------------------------------------- int8 limbs
+// Batch-1 path: the activations of one 32-slot unit are staged as three int8
+// limbs a1, a2, a3 (slot order, 4 slots per dword) and a power-of-two scale
+// s1:  x_s ~= s1 * (a1_s + a2_s / 2^7 + a3_s / 2^14), |a| <= 127, with a
+// residual below s1 * 2^-15 <= 2^-14 * max|x| / 127 of the unit.  A unit's
+// contribution  sum_g A_g P_g + B_g S_g  then needs P_g = sum x_s q_s only,
+// which is  s1 * (D1 + D2 / 2^7 + D3 / 2^14)  with D_l = sum a_l,s q_s exact
+// int32 dot products (v_dot4c_i32_i8: 4 multiply-adds per instruction).
+struct Limbs {
+    int l1[8], l2[8], l3[8];  // dword i = slots 4i..4i+3
+    float s1;
+    float S[4];
+};
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+__device__ __forceinline__ float limb_sum(int d1, int d2, int d3) {
+    return __builtin_fmaf((float)d3, 0x1p-14f, __builtin_fmaf((float)d2, 0x1p-7f, (float)d1));
+}
+// q dword holding slots 4i..4i+3 (bytes 0..127 as signed int8), group g
+template <int G>
+__device__ __forceinline__ void acc_dword(int q, int i, const Limbs& L, int (&D)[3][G], int g) {
+    D[0][g] = sdot4(q, L.l1[i], D[0][g]);
+    D[1][g] = sdot4(q, L.l2[i], D[1][g]);
+    D[2][g] = sdot4(q, L.l3[i], D[2][g]);
+}
+
+// Nibble formats (Q4_0, Q4_1, Q4_K): qs dword i -> low nibbles are slots
+// 4i..4i+3 (group 0 for Q4_K), high nibbles slots 16+4i.. (group 1 for Q4_K).
+template <int G>
+__device__ __forceinline__ void nibble_dots(const uint4& qs, const Limbs& L, int (&D)[3][G]) {
+    const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int lo = (int)(w[i] & 0x0F0F0F0Fu), hi = (int)((w[i] >> 4) & 0x0F0F0F0Fu);
+        acc_dword<G>(lo, i, L, D, 0);
+        acc_dword<G>(hi, 4 + i, L, D, G - 1);
+    }
+}
+
+template <int F>
+__device__ __forceinline__ float limb_dot(const typename Fmt<F>::Raw& r, int u, const Limbs& L);
+
+template <>
+__device__ __forceinline__ float limb_dot<Q4_0>(const Fmt<Q4_0>::Raw& r, int, const Limbs& L) {
+    int D[3][1] = {{0}, {0}, {0}};
+    nibble_dots<1>(r.qs, L, D);
+    const float d = f16_hw(r.d);
+    // d * (sum x q) - 8 d * (sum x)
+    return __builtin_fmaf(d * L.s1, limb_sum(D[0][0], D[1][0], D[2][0]), -8.0f * d * L.S[0]);
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<Q4_1>(const Fmt<Q4_1>::Raw& r, int, const Limbs& L) {
+    int D[3][1] = {{0}, {0}, {0}};
+    nibble_dots<1>(r.qs, L, D);
+    const float d = f16_hw(r.dm & 0xFFFFu), m = f16_hw(r.dm >> 16);
+    return __builtin_fmaf(d * L.s1, limb_sum(D[0][0], D[1][0], D[2][0]), m * L.S[0]);
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<Q8_0>(const Fmt<Q8_0>::Raw& r, int, const Limbs& L) {
+    int D[3][1] = {{0}, {0}, {0}};
+    const uint32_t v[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc_dword<1>((int)v[i], i, L, D, 0);
+    return f16_hw(r.d) * L.s1 * limb_sum(D[0][0], D[1][0], D[2][0]);
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<Q4_K>(const Fmt<Q4_K>::Raw& r, int u, const Limbs& L) {
+    int D[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+    nibble_dots<2>(r.qs, L, D);
+    const float d = f16_hw(r.hdr.x & 0xFFFFu), dmin = f16_hw(r.hdr.x >> 16);
+    uint32_t sa, ma, sb, mb;
+    Fmt<Q4_K>::scale_min(r.hdr, (u & 7) >> 1, sa, ma, sb, mb);
+    const float ds = d * L.s1;
+    float acc = -(dmin * (float)ma) * L.S[0];
+    acc = __builtin_fmaf(-(dmin * (float)mb), L.S[1], acc);
+    acc = __builtin_fmaf(ds * (float)sa, limb_sum(D[0][0], D[1][0], D[2][0]), acc);
+    return __builtin_fmaf(ds * (float)sb, limb_sum(D[0][1], D[1][1], D[2][1]), acc);
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<Q6_K>(const Fmt<Q6_K>::Raw& r, int u, const Limbs& L) {
+    const uint32_t a[2] = {r.ql_lo.x, r.ql_lo.y}, b[2] = {r.ql_hi.x, r.ql_hi.y},
+                   h[2] = {r.qh.x, r.qh.y};
+    int D[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q1 = (int)((a[i] & 0x0F0F0F0Fu) | ((h[i] & 0x03030303u) << 4));
+        const int q2 = (int)((b[i] & 0x0F0F0F0Fu) | ((h[i] & 0x0C0C0C0Cu) << 2));
+        const int q3 = (int)(((a[i] >> 4) & 0x0F0F0F0Fu) | (h[i] & 0x30303030u));
+        const int q4 = (int)(((b[i] >> 4) & 0x0F0F0F0Fu) | ((h[i] >> 2) & 0x30303030u));
+        acc_dword<4>(q1, 0 + i, L, D, 0);
+        acc_dword<4>(q2, 2 + i, L, D, 1);
+        acc_dword<4>(q3, 4 + i, L, D, 2);
+        acc_dword<4>(q4, 6 + i, L, D, 3);
+    }
+    // fold the int8 sub-scales in integer arithmetic: |sum_g sc_g D_g| < 2^24
+    const int is = (u & 3) >> 1;
+    int sc[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int t = is + 2 * g;
+        const uint32_t word = t < 4 ? r.sc.x : r.sc.y;
+        sc[g] = (int)(int8_t)((word >> (8 * (t & 3))) & 0xFFu);
+    }
+    int E[3];
+    float sS = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+        int e = 0;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) e = __mul24(sc[g], D[l][g]) + e;
+        E[l] = e;
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sS = __builtin_fmaf((float)sc[g], L.S[g], sS);
+    const float d = f16_hw(r.d);
+    // d * sum_g sc_g (P_g - 32 S_g)
+    return d * __builtin_fmaf(L.s1, limb_sum(E[0], E[1], E[2]), -32.0f * sS);
+}
 
 }  // namespace fq

@@ -1,21 +1,23 @@
 // fq_gemv.hip -- fused dequant + GEMV (M = 1) and small-batch (M <= 32)
-// kernels for gfx950, plus the split-K finalize and the dequant kernel.
+// kernels for gfx950, and the bit-exact dequant kernel.
 //
 // Work decomposition (one launch):
 //   grid.x  persistent work-groups striding over row groups,
 //   grid.y  K-splits (contiguous ranges of 32-weight units),
-//   grid.z  token groups of MT activations (small batch only).
-// A work-group of 256 threads (4 wave64) first stages its activation slice
-// in LDS, in the unit/slot order of the format (see fq_formats.h), together
-// with the per-group activation sums.  Then each wave takes 64/T rows at a
-// time; the T lanes of a row walk the row's units with stride T, loading each
-// unit's bytes straight from HBM (one or two wide loads per unit, consecutive
-// lanes on consecutive units, so a row segment is read contiguously), decode
-// nibbles/bytes in registers and FMA against conflict-free ds_read_b128 of
-// the staged activations.  The T partial sums of a row are combined with
-// cross-lane shuffles inside the wave; no LDS round-trip, no atomics, so the
-// result is deterministic.  With more than one K-split the per-split
-// partials go to a workspace and fq_finalize sums them in split order.
+//   grid.z  token groups of MT activations.
+// A work-group of 256 threads (4 wave64) owns 16 rows per step: each wave
+// takes 64/T rows and the T lanes of a row own units li, li+T, ... of the
+// row (at most NU per lane).  Per step a lane first issues the wide loads of
+// ALL its units (consecutive lanes on consecutive units, so each row segment
+// streams contiguously) and only then waits, decodes and FMAs against the
+// activations staged in LDS; the very first step's loads are issued before
+// the activations are staged, so staging overlaps the first HBM round trip,
+// and each later step's loads are issued before the previous step's
+// reduction and stores.  The T partial sums of a row are combined with
+// cross-lane shuffles inside the wave: no LDS round trip and no atomics on
+// y, so results are deterministic.  With several K-splits each split writes
+// its partial row sums to a workspace and the last split to arrive for a
+// row group (device counter) adds them in split order and writes y.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -25,6 +27,7 @@
 namespace fq {
 
 constexpr int WG = 256;
+constexpr int RPB = 16;  // rows per work-group step (4 waves x 64/T rows; T = 16)
 
 template <int T>
 __device__ __forceinline__ float row_reduce(float v) {
@@ -103,77 +106,111 @@ __device__ __forceinline__ void unit_dot(const typename Fmt<F>::Raw& raw, int u_
     }
 }
 
-template <int F, int T, int MT>
+template <int F, int T, int NU>
+__device__ __forceinline__ void load_units(typename Fmt<F>::Raw* raw, const uint8_t* __restrict__ w,
+                                           int row, int N, int row_bytes, int u0, int uc,
+                                           int li) {
+    if (row < N) {
+        const uint8_t* wr = w + (size_t)row * row_bytes;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int uu = li + i * T;
+            if (uu < uc) raw[i] = Fmt<F>::load(wr, u0 + uu);
+        }
+    }
+}
+
+template <int F, int T, int MT, int NU>
 __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
     extern __shared__ float lds[];
-    using Fm = Fmt<F>;
-    constexpr int RPW = 64 / T;            // rows per wave per step
-    constexpr int RPB = (WG / 64) * RPW;   // rows per work-group per step
+    using Raw = typename Fmt<F>::Raw;
+    constexpr int RPW = 64 / T;
+    static_assert(RPW * (WG / 64) == RPB, "16 rows per work-group step");
+    __shared__ int last_flag;
+
     const int m0 = blockIdx.z * MT;
     const int mt = min(MT, a.M - m0);
     const int u0 = blockIdx.y * a.Uc;
     const int uc = min(a.Uc, a.U - u0);
-    stage_x<F, MT>(lds, a.x, a.K, m0, mt, u0, uc);
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane % T, rsub = lane / T;
-    for (int rg = blockIdx.x; rg * RPB < a.N; rg += gridDim.x) {
+    const int S = gridDim.y;
+
+    Raw raw[NU];
+    int rg = blockIdx.x;
+    // the first step's weight loads go out before the activations are staged
+    load_units<F, T, NU>(raw, a.w, rg * RPB + wave * RPW + rsub, a.N, a.row_bytes, u0, uc, li);
+    stage_x<F, MT>(lds, a.x, a.K, m0, mt, u0, uc);
+
+    for (; rg * RPB < a.N; rg += gridDim.x) {
         const int row = rg * RPB + wave * RPW + rsub;
         float acc[MT];
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
         if (row < a.N) {
-            const uint8_t* wr = a.w + (size_t)row * a.row_bytes;
-            int uu = li;
-            // two units in flight per lane: issue both loads, then compute
-            for (; uu + T < uc; uu += 2 * T) {
-                auto r0 = Fm::load(wr, u0 + uu);
-                auto r1 = Fm::load(wr, u0 + uu + T);
-                unit_dot<F, MT>(r0, u0 + uu, uu, uc, lds, acc);
-                unit_dot<F, MT>(r1, u0 + uu + T, uu + T, uc, lds, acc);
-            }
-            if (uu < uc) {
-                auto r0 = Fm::load(wr, u0 + uu);
-                unit_dot<F, MT>(r0, u0 + uu, uu, uc, lds, acc);
+#pragma unroll
+            for (int i = 0; i < NU; ++i) {
+                const int uu = li + i * T;
+                if (uu < uc) unit_dot<F, MT>(raw[i], u0 + uu, uu, uc, lds, acc);
             }
         }
+        // the next step's loads fly during the reduction and the stores
+        const int rg_next = rg + gridDim.x;
+        if (rg_next * RPB < a.N)
+            load_units<F, T, NU>(raw, a.w, rg_next * RPB + wave * RPW + rsub, a.N, a.row_bytes,
+                                 u0, uc, li);
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[t] = row_reduce<T>(acc[t]);
-        if (li == 0 && row < a.N) {
-            for (int t = 0; t < mt; ++t) {
-                const int m = m0 + t;
-                if (a.part) {
-                    a.part[((size_t)blockIdx.y * a.M + m) * a.N + row] = acc[t];
-                } else {
+
+        if (S == 1) {
+            if (li == 0 && row < a.N) {
+                for (int t = 0; t < mt; ++t) {
+                    const int m = m0 + t;
                     float v = acc[t];
                     if (a.bias_mode == 1) {
                         if (row < a.bias_len) v += a.bias[row];
                     } else if (a.bias_mode == 2) {
-                        size_t i = (size_t)m * a.N + row;
+                        const size_t i = (size_t)m * a.N + row;
                         if ((int64_t)i < a.bias_len) v += a.bias[i];
                     }
                     a.y[(size_t)m * a.N + row] = v;
                 }
             }
+            continue;
         }
-    }
-}
-
-// y[m][n] = sum_s part[s][m][n] (+ bias), split order fixed.
-__global__ __launch_bounds__(256) void finalize_kernel(const float* __restrict__ part, float* y,
-                                                       int S, int M, int N, const float* bias,
-                                                       int bias_mode, int64_t bias_len) {
-    const size_t MN = (size_t)M * N;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
-        float v = 0.0f;
-        for (int s = 0; s < S; ++s) v += part[s * MN + i];
-        const int n = (int)(i % N);
-        if (bias_mode == 1) {
-            if (n < bias_len) v += bias[n];
-        } else if (bias_mode == 2) {
-            if ((int64_t)i < bias_len) v += bias[i];
+        // ---- split-K: publish partials; the last split of this row group reduces
+        if (li == 0 && row < a.N) {
+            for (int t = 0; t < mt; ++t)
+                a.part[((size_t)blockIdx.y * a.M + m0 + t) * a.N + row] = acc[t];
         }
-        y[i] = v;
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned* cnt = a.counters + (size_t)blockIdx.z * a.rg_total + rg;
+            const unsigned old = atomicAdd(cnt, 1u);
+            const int is_last = old == (unsigned)(S - 1);
+            if (is_last) atomicExch(cnt, 0u);  // leave the counter zeroed for the next call
+            last_flag = is_last;
+        }
+        __syncthreads();
+        if (last_flag) {
+            __threadfence();
+            for (int i = threadIdx.x; i < RPB * mt; i += WG) {
+                const int r = rg * RPB + (i % RPB), t = i / RPB;
+                if (r >= a.N) continue;
+                const int m = m0 + t;
+                float v = 0.0f;
+                for (int s = 0; s < S; ++s)
+                    v += __builtin_nontemporal_load(&a.part[((size_t)s * a.M + m) * a.N + r]);
+                if (a.bias_mode == 1) {
+                    if (r < a.bias_len) v += a.bias[r];
+                } else if (a.bias_mode == 2) {
+                    const size_t j = (size_t)m * a.N + r;
+                    if ((int64_t)j < a.bias_len) v += a.bias[j];
+                }
+                a.y[(size_t)m * a.N + r] = v;
+            }
+        }
     }
 }
 
@@ -201,78 +238,56 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
     }
 }
 
+// Clears n words (used instead of a memset node, so callers may capture it).
+__global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        p[i] = 0u;
+}
+
 // ---------------------------------------------------------------- launchers
-template <int F, int T, int MT>
-static hipError_t launch_t(const GemvArgs& a, const LaunchCfg& c, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_kernel<F, T, MT>), dim3(c.grid_x, c.splits, c.token_groups), dim3(WG),
-                       c.lds_bytes, st, a);
-    return hipGetLastError();
-}
-
 template <int F, int MT>
-static hipError_t launch_mt(const GemvArgs& a, const LaunchCfg& c, hipStream_t st) {
-    switch (c.T) {
-        case 16: return launch_t<F, 16, MT>(a, c, st);
-        case 64: return launch_t<F, 64, MT>(a, c, st);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-template <int F>
-static hipError_t launch_f(const GemvArgs& a, const LaunchCfg& c, hipStream_t st) {
-    switch (c.MT) {
-        case 1: return launch_mt<F, 1>(a, c, st);
-        case 2: return launch_mt<F, 2>(a, c, st);
-        case 4: return launch_mt<F, 4>(a, c, st);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-hipError_t launch_gemv(int dtype, const GemvArgs& a, const LaunchCfg& c, hipStream_t st) {
-    switch (dtype) {
-        case Q4_0: return launch_f<Q4_0>(a, c, st);
-        case Q4_1: return launch_f<Q4_1>(a, c, st);
-        case Q8_0: return launch_f<Q8_0>(a, c, st);
-        case Q4_K: return launch_f<Q4_K>(a, c, st);
-        case Q6_K: return launch_f<Q6_K>(a, c, st);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-template <int F, int T, int MT>
-static const void* fn_t() {
-    return reinterpret_cast<const void*>(&gemv_kernel<F, T, MT>);
-}
-
-template <int F>
-static const void* fn_f(int T, int MT) {
-    if (T == 16) {
-        if (MT == 1) return fn_t<F, 16, 1>();
-        if (MT == 2) return fn_t<F, 16, 2>();
-        if (MT == 4) return fn_t<F, 16, 4>();
-    } else if (T == 64) {
-        if (MT == 1) return fn_t<F, 64, 1>();
-        if (MT == 2) return fn_t<F, 64, 2>();
-        if (MT == 4) return fn_t<F, 64, 4>();
-    }
-    return nullptr;
-}
-
-const void* gemv_kernel_fn(int dtype, int T, int MT) {
-    switch (dtype) {
-        case Q4_0: return fn_f<Q4_0>(T, MT);
-        case Q4_1: return fn_f<Q4_1>(T, MT);
-        case Q8_0: return fn_f<Q8_0>(T, MT);
-        case Q4_K: return fn_f<Q4_K>(T, MT);
-        case Q6_K: return fn_f<Q6_K>(T, MT);
+static const void* kfn_mt(int NU) {
+    switch (NU) {
+        case 2: return reinterpret_cast<const void*>(&gemv_kernel<F, 16, MT, 2>);
+        case 4: return reinterpret_cast<const void*>(&gemv_kernel<F, 16, MT, 4>);
+        case 8: return reinterpret_cast<const void*>(&gemv_kernel<F, 16, MT, 8>);
         default: return nullptr;
     }
 }
 
-hipError_t launch_finalize(const float* part, float* y, int S, int M, int N, const float* bias,
-                           int bias_mode, int64_t bias_len, int grid, hipStream_t st) {
-    hipLaunchKernelGGL(finalize_kernel, dim3(grid), dim3(256), 0, st, part, y, S, M, N, bias,
-                       bias_mode, bias_len);
+template <int F>
+static const void* kfn_f(int MT, int NU) {
+    switch (MT) {
+        case 1: return kfn_mt<F, 1>(NU);
+        case 2: return kfn_mt<F, 2>(NU);
+        case 4: return kfn_mt<F, 4>(NU);
+        default: return nullptr;
+    }
+}
+
+const void* gemv_kernel_fn(int dtype, int T, int MT, int NU) {
+    if (T != 16) return nullptr;
+    switch (dtype) {
+        case Q4_0: return kfn_f<Q4_0>(MT, NU);
+        case Q4_1: return kfn_f<Q4_1>(MT, NU);
+        case Q8_0: return kfn_f<Q8_0>(MT, NU);
+        case Q4_K: return kfn_f<Q4_K>(MT, NU);
+        case Q6_K: return kfn_f<Q6_K>(MT, NU);
+        default: return nullptr;
+    }
+}
+
+hipError_t launch_gemv(int dtype, const GemvArgs& a, const LaunchCfg& c, hipStream_t st) {
+    const void* fn = gemv_kernel_fn(dtype, c.T, c.MT, c.NU);
+    if (!fn) return hipErrorInvalidValue;
+    GemvArgs args = a;
+    void* params[] = {&args};
+    return hipLaunchKernel(fn, dim3(c.grid_x, c.splits, c.token_groups), dim3(WG), params,
+                           c.lds_bytes, st);
+}
+
+hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st) {
+    hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(256), 0, st, p, n);
     return hipGetLastError();
 }
 

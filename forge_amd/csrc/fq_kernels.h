@@ -12,6 +12,8 @@ struct GemvArgs {
     const uint8_t* w;     // [N] rows of row_bytes
     float* y;             // [M][N]
     float* part;          // [splits][M][N] when splits > 1, else nullptr
+    unsigned* counters;   // [token_groups][rg_total] split arrival counters (zero between calls)
+    int rg_total;         // row groups of 16 rows: ceil(N / 16)
     const float* bias;    // optional, see bias_mode
     int64_t bias_len;
     int bias_mode;        // 0 none, 1 row vector over n, 2 full [M][N]
@@ -22,8 +24,9 @@ struct GemvArgs {
 };
 
 struct LaunchCfg {
-    int T;                // lanes per row: 16 or 64
+    int T;                // lanes per row (16)
     int MT;               // tokens per work-group: 1, 2 or 4
+    int NU;               // max units per lane per row: 2, 4 or 8
     int grid_x;           // persistent work-groups per (split, token group)
     int splits;           // grid.y
     int token_groups;     // grid.z
@@ -31,9 +34,16 @@ struct LaunchCfg {
 };
 
 hipError_t launch_gemv(int dtype, const GemvArgs& a, const LaunchCfg& c, hipStream_t st);
-const void* gemv_kernel_fn(int dtype, int T, int MT);
-hipError_t launch_finalize(const float* part, float* y, int S, int M, int N, const float* bias,
-                           int bias_mode, int64_t bias_len, int grid, hipStream_t st);
+const void* gemv_kernel_fn(int dtype, int T, int MT, int NU);
+// batch-1 persistent kernel (fq_gemv1.hip)
+const void* gemv1_kernel_fn(int dtype, bool bias, int wg);
+size_t gemv1_lds_bytes(int dtype, int U, int wg);
+hipError_t launch_gemv1(int dtype, const GemvArgs& a, int grid, int wg, hipStream_t st);
+const void* gemv1r_kernel_fn(int dtype, int U, int row_bytes, bool bias, int* npr_out,
+                             size_t* lds_out, int* wg_out);
+hipError_t launch_raw(const void* fn, const GemvArgs& a, int grid, int wg, size_t lds,
+                      hipStream_t st);
+hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st);
 hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,
                           int row_bytes, int grid, hipStream_t st);
 
