@@ -18,6 +18,7 @@ FQ_ERR_SHAPE = 2
 FQ_ERR_NULL = 3
 FQ_ERR_HIP = 4
 FQ_ERR_NO_DEVICE = 5
+FQ_ERR_ALIGN = 6
 
 # Every symbol include/forge_q.h declares, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -33,6 +34,10 @@ SIGNATURES = {
     "fq_matmul_prefill": (_I, [_U, _P, _P, _P, _I, _I, _I, _P]),
     "fq_matmul_transB": (_I, [_U, _P, _P, _P, _I, _L, _P, _I, _I, _I, _P]),
     "fq_dequant_rows": (_I, [_U, _P, _P, _I, _I, _P]),
+    "fq_packed_row_bytes": (_L, [_U, _I]),
+    "fq_pack_weights": (_I, [_U, _P, _P, _I, _I, _P]),
+    "fq_unpack_weights": (_I, [_U, _P, _P, _I, _I, _P]),
+    "fq_gemv_packed": (_I, [_U, _P, _P, _P, _L, _P, _I, _I, _P]),
 }
 
 _lib = None

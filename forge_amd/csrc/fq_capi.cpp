@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <climits>
 #include <cstdlib>
+#include <cstdio>
 #include <cstdint>
 #include <map>
 #include <mutex>
@@ -16,6 +17,7 @@
 
 #include "../../include/forge_q.h"
 #include "fq_kernels.h"
+#include "fq_pack.h"
 
 namespace {
 
@@ -279,6 +281,7 @@ const char* fq_status_str(int status) {
         case FQ_ERR_NULL: return "null pointer";
         case FQ_ERR_HIP: return "HIP runtime error";
         case FQ_ERR_NO_DEVICE: return "no HIP device";
+        case FQ_ERR_ALIGN: return "packed buffer not 16-byte aligned";
         default: return "unknown status";
     }
 }
@@ -331,6 +334,94 @@ int fq_dequant_rows(uint32_t dtype, const void* w, float* out, int N, int K, voi
     int grid = (int)std::min<size_t>((total + 255) / 256, (size_t)di.cus * 16);
     e = fq::launch_dequant((int)dtype, static_cast<const uint8_t*>(w), out, N, K, U,
                            nblk * g.bb, grid, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? FQ_OK : hip_fail(e);
+}
+
+int64_t fq_packed_row_bytes(uint32_t dtype, int K) {
+    Geometry g;
+    if (!geometry(dtype, g) || K <= 0 || K % 256 != 0) return 0;
+    return fq::packed_row_bytes((int)dtype, K);
+}
+
+static int pack_common(uint32_t dtype, const void* src, void* dst, int N, int K, bool pack,
+                       void* stream) {
+    Geometry g;
+    if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
+    if (N < 0 || K < 0 || K % 256 != 0) return FQ_ERR_SHAPE;
+    if (N == 0 || K == 0) return FQ_OK;
+    if (!src || !dst) return FQ_ERR_NULL;
+    const void* packed = pack ? dst : src;
+    const void* gguf = pack ? src : dst;
+    if ((reinterpret_cast<uintptr_t>(packed) & 15) != 0) return FQ_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(gguf) & 1) != 0) return FQ_ERR_ALIGN;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    const DevInfo di = device_info(dev);
+    e = fq::launch_pack((int)dtype, static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst),
+                        N, K, pack, di.cus * 8, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? FQ_OK : hip_fail(e);
+}
+
+int fq_pack_weights(uint32_t dtype, const void* w_gguf, void* w_packed, int N, int K,
+                    void* stream) {
+    return pack_common(dtype, w_gguf, w_packed, N, K, true, stream);
+}
+
+int fq_unpack_weights(uint32_t dtype, const void* w_packed, void* w_gguf, int N, int K,
+                      void* stream) {
+    return pack_common(dtype, w_packed, w_gguf, N, K, false, stream);
+}
+
+
+int fq_gemv_packed(uint32_t dtype, const float* x, const void* w_packed, const float* bias,
+                   int64_t bias_len, float* y, int K, int N, void* stream) {
+    Geometry g;
+    if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
+    if (N < 0 || K < 0 || K % 256 != 0) return FQ_ERR_SHAPE;
+    if (N == 0) return FQ_OK;
+    if (!x || !w_packed || !y) return FQ_ERR_NULL;
+    if ((reinterpret_cast<uintptr_t>(w_packed) & 15) != 0) return FQ_ERR_ALIGN;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    const DevInfo di = device_info(dev);
+    if (K == 0) {
+        if (bias) return FQ_ERR_SHAPE;
+        e = fq::launch_zero(reinterpret_cast<uint32_t*>(y), (size_t)N, di.cus, st);
+        return e == hipSuccess ? FQ_OK : hip_fail(e);
+    }
+    int units = 0, records = 0;
+    fq::gemvp_geometry((int)dtype, K, &units, &records);
+    size_t lds = 0;
+    int wg = 0;
+    const void* fn = fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg);
+    if (!fn || lds > std::min<size_t>(di.lds, 160 * 1024)) return FQ_ERR_SHAPE;
+    int per_cu = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wg, lds);
+    if (e != hipSuccess) return hip_fail(e);
+    if (per_cu < 1) return FQ_ERR_SHAPE;
+    const int wpb = wg / 64;
+    // one work-group per resident slot, each owning a contiguous row range of
+    // at most 4096 rows (its LDS result buffer) and at least one row per wave
+    long G = (long)di.cus * per_cu;
+    G = std::max(1L, std::min<long>(G, ((long)N + wpb - 1) / wpb));
+    G = std::max<long>(G, ((long)N + 4095) / 4096);
+    fq::GemvArgs a{};
+    a.x = x;
+    a.w = static_cast<const uint8_t*>(w_packed);
+    a.y = y;
+    a.bias = bias;
+    a.bias_len = bias ? bias_len : 0;
+    a.bias_mode = bias ? 1 : 0;
+    a.M = 1;
+    a.K = K;
+    a.N = N;
+    a.U = units;
+    a.Uc = records;
+    a.row_bytes = (int)fq::packed_row_bytes((int)dtype, K);
+    e = fq::launch_raw(fn, a, (int)G, wg, lds, st);
     return e == hipSuccess ? FQ_OK : hip_fail(e);
 }
 

@@ -35,31 +35,22 @@ enum : int { Q4_0 = 2, Q4_1 = 3, Q4_K = 4, Q8_0 = 7, Q6_K = 13 };
 typedef uint32_t fq_u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t fq_u32x4 __attribute__((ext_vector_type(4)));
 
-#if defined(FQ_PROBE_ALIGNED)
-#define FQ_ALIGN_PROBE(p) ((p) - (reinterpret_cast<uintptr_t>(p) & 15))
-#else
-#define FQ_ALIGN_PROBE(p) (p)
-#endif
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
-    p = FQ_ALIGN_PROBE(p);
     uint16_t v;
     __builtin_memcpy(&v, p, 2);
     return v;
 }
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
-    p = FQ_ALIGN_PROBE(p);
     uint32_t v;
     __builtin_memcpy(&v, p, 4);
     return v;
 }
 __device__ __forceinline__ uint2 ld_u64(const uint8_t* p) {
-    p = FQ_ALIGN_PROBE(p);
     uint2 v;
     __builtin_memcpy(&v, p, 8);
     return v;
 }
 __device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
-    p = FQ_ALIGN_PROBE(p);
     uint4 v;
     __builtin_memcpy(&v, p, 16);
     return v;

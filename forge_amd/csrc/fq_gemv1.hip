@@ -21,84 +21,11 @@
 
 #include "fq_formats.h"
 #include "fq_kernels.h"
+#include "fq_limbs.h"
 
 namespace fq {
 namespace {
 
-
-// Full 64-lane sum; the result is valid in lane 63.
-__device__ __forceinline__ float wave_sum(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false));
-    return v;
-}
-
-// Stage x as int8 limbs (see Limbs in fq_formats.h).  Record of unit u at
-// byte 144*u: a1[32] @0, a2[32] @32, a3[32] @64, s1 @96, S[4] @100.  The 32
-// lanes of a half-wave handle one unit: max |x| and the group sums are
-// shuffle trees inside those 32 lanes (fixed order, so deterministic).
-constexpr int RECB = 144;
-
-template <int F, int WG1>
-__device__ __forceinline__ void stage_limbs(uint8_t* lds, const float* __restrict__ x, int U) {
-    using Fm = Fmt<F>;
-    constexpr int NG = Fm::NG, GS = 32 / NG, XB = 8;
-    const int total = 32 * U;
-    for (int base = 0; base < total; base += XB * WG1) {
-        float v[XB];
-#pragma unroll
-        for (int j = 0; j < XB; ++j) {  // clamped, unconditional loads
-            const int idx = min(base + j * WG1 + (int)threadIdx.x, total - 1);
-            v[j] = x[Fm::k_of(idx >> 5, idx & 31)];
-        }
-#pragma unroll
-        for (int j = 0; j < XB; ++j) {
-            const int idx = base + j * WG1 + (int)threadIdx.x;
-            if (base + j * WG1 >= total) break;  // uniform across the work-group
-            const bool live = idx < total;
-            const float xv = live ? v[j] : 0.0f;
-            float m = __builtin_fabsf(xv);
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
-            int e = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu);
-            e = max(e, 21);  // keeps s1 * 2^-14 a normal number
-            float s1 = __builtin_bit_cast(float, (uint32_t)(e - 6) << 23);
-            if (m >= 127.5f * s1) {
-                ++e;
-                s1 *= 2.0f;
-            }
-            const float inv = __builtin_bit_cast(float, (uint32_t)(254 - (e - 6)) << 23);
-            const float a1 = __builtin_rintf(xv * inv);
-            const float r1 = __builtin_fmaf(-a1, s1, xv);
-            const float a2 = __builtin_rintf(r1 * (inv * 128.0f));
-            const float r2 = __builtin_fmaf(-a2, s1 * 0x1p-7f, r1);
-            const float a3 = __builtin_rintf(r2 * (inv * 16384.0f));
-            if (!(m <= 3.0e38f)) s1 = __builtin_nanf("");  // Inf/NaN in x propagates
-            float gs = xv;
-#pragma unroll
-            for (int off = GS / 2; off > 0; off >>= 1) gs += __shfl_xor(gs, off, 32);
-            if (live) {
-                const int u = idx >> 5, sl = idx & 31;
-                uint8_t* rec = lds + RECB * u;
-                rec[sl] = (uint8_t)(int8_t)(int)a1;
-                rec[32 + sl] = (uint8_t)(int8_t)(int)a2;
-                rec[64 + sl] = (uint8_t)(int8_t)(int)a3;
-                if (sl == 0) *reinterpret_cast<float*>(rec + 96) = s1;
-                if (NG > 0 && (sl % GS) == 0) reinterpret_cast<float*>(rec + 100)[sl / GS] = gs;
-            }
-        }
-    }
-    __syncthreads();
-}
-
-// The bias is read through the constant address space with a wave-uniform
-// index, i.e. with a scalar load: it does not join the vector-memory queue,
-// so adding it never waits on weight fetches in flight.
-typedef const __attribute__((address_space(4))) float* const_fp;
 
 template <int F>
 __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int u,
@@ -203,11 +130,7 @@ __device__ __forceinline__ void consume(const GemvArgs& a, const Pos& p, const u
     const int nunits = min(64, a.U - 64 * p.c);
     const int ul = min(lane, nunits - 1);
     const auto raw = Fmt<F>::template load<false>(wbuf + shift, ul);
-#if defined(FQ_PROBE_NO_DOT)
-    const float t = acc + (float)(reinterpret_cast<const uint32_t*>(&raw)[0] & 1u);
-#else
     const float t = unit_dot1<F>(raw, 64 * p.c + ul, lds, acc);
-#endif
     acc = lane < nunits ? t : acc;
     const bool row_end = p.c == nc - 1;  // wave-uniform
     float s = __builtin_bit_cast(
@@ -248,13 +171,15 @@ __global__ __launch_bounds__(WG1) void gemv1_kernel(GemvArgs a) {
 
     // two chunks in flight per wave; the first two are fetched before the
     // activations are staged
+    XStage<Fmt<F>, WG1> xs;
+    stage_load<Fmt<F>, WG1>(xs, a.x, a.U, 0);  // activation loads before weight loads
     Pos ld{first, 0}, cp{first, 0};
     Fetch<F> f0, f1;
     fetch<F>(f0, a, ld, lane);
     ld.next(nc, stride);
     fetch<F>(f1, a, ld, lane);
     ld.next(nc, stride);
-    stage_limbs<F, WG1>(lds, a.x, a.U);
+    stage_build<Fmt<F>, WG1>(lds, xs, a.x, a.U, 0);
 
     float acc = 0.0f;
     while (cp.row < a.N) {
@@ -309,23 +234,6 @@ __device__ __forceinline__ void rspill(const RowFetch<NPR>& f, uint8_t* wbuf, in
     for (int i = 0; i < NPR; ++i) reinterpret_cast<uint4*>(wbuf)[lane + 64 * i] = f.v[i];
 }
 
-__device__ __forceinline__ void read_limbs(Limbs& L, const uint8_t* lds, int u) {
-    const int4* rp = reinterpret_cast<const int4*>(lds + RECB * u);
-    const int4 v0 = rp[0], v1 = rp[1], v2 = rp[2], v3 = rp[3], v4 = rp[4], v5 = rp[5];
-    L.l1[0] = v0.x; L.l1[1] = v0.y; L.l1[2] = v0.z; L.l1[3] = v0.w;
-    L.l1[4] = v1.x; L.l1[5] = v1.y; L.l1[6] = v1.z; L.l1[7] = v1.w;
-    L.l2[0] = v2.x; L.l2[1] = v2.y; L.l2[2] = v2.z; L.l2[3] = v2.w;
-    L.l2[4] = v3.x; L.l2[5] = v3.y; L.l2[6] = v3.z; L.l2[7] = v3.w;
-    L.l3[0] = v4.x; L.l3[1] = v4.y; L.l3[2] = v4.z; L.l3[3] = v4.w;
-    L.l3[4] = v5.x; L.l3[5] = v5.y; L.l3[6] = v5.z; L.l3[7] = v5.w;
-    const float4 t = reinterpret_cast<const float4*>(lds + RECB * u)[6];
-    L.s1 = t.x;
-    L.S[0] = t.y;
-    L.S[1] = t.z;
-    L.S[2] = t.w;
-    L.S[3] = reinterpret_cast<const float*>(lds + RECB * u)[28];
-}
-
 template <int F, int NC, int NPR, bool BIAS>
 __device__ __forceinline__ void row_step(RowFetch<NPR>& f, int row, int prefetch_row,
                                          const GemvArgs& a, uint8_t* wbuf, const Limbs* L,
@@ -364,10 +272,12 @@ __global__ __launch_bounds__(WG) void gemv1r_kernel(GemvArgs a) {
     uint8_t* wbuf = lds + (size_t)a.U * RECB + wave * (NPR * 1024);
 
     // D rows in flight per wave: buffer i always holds row (next + i * stride)
+    XStage<Fmt<F>, WG> xs;
+    stage_load<Fmt<F>, WG>(xs, a.x, a.U, 0);  // activation loads before weight loads
     RowFetch<NPR> f[D];
 #pragma unroll
     for (int i = 0; i < D; ++i) rfetch<NPR>(f[i], a, first + i * stride, lane);
-    stage_limbs<F, WG>(lds, a.x, a.U);
+    stage_build<Fmt<F>, WG>(lds, xs, a.x, a.U, 0);
     Limbs L[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) read_limbs(L[c], lds, min(lane + 64 * c, a.U - 1));

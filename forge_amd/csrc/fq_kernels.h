@@ -21,6 +21,8 @@ struct GemvArgs {
     int U;                // 32-weight units per row (K / 32)
     int Uc;               // units per K-split
     int row_bytes;
+    int split_units;      // packed split-K: lane units per K-slice
+    int waves_total;      // packed split-K: counter stride (waves in the grid)
 };
 
 struct LaunchCfg {
@@ -43,6 +45,11 @@ const void* gemv1r_kernel_fn(int dtype, int U, int row_bytes, bool bias, int* np
                              size_t* lds_out, int* wg_out);
 hipError_t launch_raw(const void* fn, const GemvArgs& a, int grid, int wg, size_t lds,
                       hipStream_t st);
+// packed-layout batch-1 kernels (fq_gemvp.hip)
+void gemvp_geometry(int dtype, int K, int* units, int* records);
+const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg);
+hipError_t launch_pack(int dtype, const uint8_t* src, uint8_t* dst, int N, int K, bool pack,
+                       int grid, hipStream_t st);
 hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st);
 hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,
                           int row_bytes, int grid, hipStream_t st);

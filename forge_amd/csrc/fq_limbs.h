@@ -1,0 +1,171 @@
+// fq_limbs.h -- activation staging shared by the batch-1 kernels: the int8
+// limb records (see Limbs in fq_formats.h), the 64-lane DPP sum and the
+// scalar-path bias pointer type.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fq_formats.h"
+
+namespace fq {
+
+// Full 64-lane sum; the result is valid in lane 63.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false));
+    return v;
+}
+
+// Stage x as int8 limbs (see Limbs in fq_formats.h).  Record of unit u at
+// byte 144*u: a1[32] @0, a2[32] @32, a3[32] @64, s1 @96, S[4] @100.  Eight
+// lanes build one record: lane i owns slots 4i .. 4i+3, which are four
+// consecutive activations for every format (one float4 load), and writes one
+// aligned dword of each limb.  The unit max and the group sums are all-reduce
+// trees over the eight lanes in DPP (quad_perm, row_half_mirror): no LDS
+// traffic and a fixed order, so the staging is deterministic.
+//
+// Staging is split in two so the caller can put the first weight loads
+// between them: stage_load() issues every activation load first (they are
+// then older than the weight loads in the in-order memory counter, so
+// stage_build() never waits for weight bytes), stage_build() computes and
+// writes the records.
+constexpr int RECB = 144;
+constexpr int XPMAX = 10;  // activation loads a thread keeps in flight
+
+template <class Fm>
+__device__ __forceinline__ float4 stage_x4(const float* __restrict__ x, int w0, int t) {
+    const int w = t >> 3, i = t & 7;
+    return *reinterpret_cast<const float4*>(x + Fm::k_of(w0 + w, 4 * i));
+}
+
+template <class Fm, int WG>
+struct XStage {
+    float4 v[XPMAX];
+};
+
+template <class Fm, int WG>
+__device__ __forceinline__ void stage_load(XStage<Fm, WG>& st, const float* __restrict__ x,
+                                           int nrec, int w0) {
+    const int tasks = 8 * nrec;
+#pragma unroll
+    for (int p = 0; p < XPMAX; ++p)
+        st.v[p] = stage_x4<Fm>(x, w0, min(p * WG + (int)threadIdx.x, tasks - 1));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                          0xf, 0xf, false));
+}
+
+// all-reduce over aligned groups of 2, 4 or 8 lanes
+template <int LANES>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f<0xB1>(v);                      // quad_perm [1,0,3,2]
+    if (LANES >= 4) v += dpp_f<0x4E>(v);      // quad_perm [2,3,0,1]
+    if (LANES >= 8) v += dpp_f<0x141>(v);     // row_half_mirror
+    return v;
+}
+__device__ __forceinline__ float group_max8(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
+    return ((uint32_t)(int)a & 0xFFu) | (((uint32_t)(int)b & 0xFFu) << 8) |
+           (((uint32_t)(int)c & 0xFFu) << 16) | ((uint32_t)(int)d << 24);
+}
+
+template <class Fm>
+__device__ __forceinline__ void build_task(uint8_t* lds, float4 xv, int t, int tasks) {
+    constexpr int NG = Fm::NG, GS = 32 / NG;
+    const int i = t & 7;
+    float m = fmaxf(fmaxf(__builtin_fabsf(xv.x), __builtin_fabsf(xv.y)),
+                    fmaxf(__builtin_fabsf(xv.z), __builtin_fabsf(xv.w)));
+    m = group_max8(m);
+    int e = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu);
+    e = max(e, 21);  // keeps s1 * 2^-14 a normal number
+    float s1 = __builtin_bit_cast(float, (uint32_t)(e - 6) << 23);
+    if (m >= 127.5f * s1) {
+        ++e;
+        s1 *= 2.0f;
+    }
+    const float inv = __builtin_bit_cast(float, (uint32_t)(254 - (e - 6)) << 23);
+    const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+    float a1[4], a2[4], a3[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        a1[j] = __builtin_rintf(xs[j] * inv);
+        const float r1 = __builtin_fmaf(-a1[j], s1, xs[j]);
+        a2[j] = __builtin_rintf(r1 * (inv * 128.0f));
+        const float r2 = __builtin_fmaf(-a2[j], s1 * 0x1p-7f, r1);
+        a3[j] = __builtin_rintf(r2 * (inv * 16384.0f));
+    }
+    if (!(m <= 3.0e38f)) s1 = __builtin_nanf("");  // Inf/NaN in x propagates
+    float gs = (xv.x + xv.y) + (xv.z + xv.w);
+    if (GS >= 8) gs = group_sum<GS / 4>(gs);
+    if (t < tasks) {
+        uint8_t* rec = lds + RECB * (t >> 3);
+        reinterpret_cast<uint32_t*>(rec)[i] = pack4(a1[0], a1[1], a1[2], a1[3]);
+        reinterpret_cast<uint32_t*>(rec + 32)[i] = pack4(a2[0], a2[1], a2[2], a2[3]);
+        reinterpret_cast<uint32_t*>(rec + 64)[i] = pack4(a3[0], a3[1], a3[2], a3[3]);
+        if (i == 0) *reinterpret_cast<float*>(rec + 96) = s1;
+        if ((4 * i) % GS == 0) reinterpret_cast<float*>(rec + 100)[(4 * i) / GS] = gs;
+    }
+}
+
+template <class Fm, int WG>
+__device__ __forceinline__ void stage_build(uint8_t* lds, const XStage<Fm, WG>& st,
+                                            const float* __restrict__ x, int nrec, int w0) {
+    const int tasks = 8 * nrec;
+#pragma unroll
+    for (int p = 0; p < XPMAX; ++p) {
+        if (p * WG < tasks) build_task<Fm>(lds, st.v[p], p * WG + (int)threadIdx.x, tasks);
+    }
+    // rows longer than XPMAX * WG / 8 records: the rest, loaded and built in turn
+    for (int base = XPMAX * WG; base < tasks; base += WG) {
+        const int t = base + (int)threadIdx.x;
+        build_task<Fm>(lds, stage_x4<Fm>(x, w0, min(t, tasks - 1)), t, tasks);
+    }
+    __syncthreads();
+}
+
+// One-call form for kernels with nothing to overlap.
+template <class Fm, int WG>
+__device__ __forceinline__ void stage_limbs(uint8_t* lds, const float* __restrict__ x, int nrec,
+                                            int w0 = 0) {
+    XStage<Fm, WG> st;
+    stage_load<Fm, WG>(st, x, nrec, w0);
+    stage_build<Fm, WG>(lds, st, x, nrec, w0);
+}
+
+// The bias is read through the constant address space with a wave-uniform
+// index, i.e. with a scalar load: it does not join the vector-memory queue,
+// so adding it never waits on weight fetches in flight.
+typedef const __attribute__((address_space(4))) float* const_fp;
+
+__device__ __forceinline__ void read_limbs(Limbs& L, const uint8_t* lds, int u) {
+    const int4* rp = reinterpret_cast<const int4*>(lds + RECB * u);
+    const int4 v0 = rp[0], v1 = rp[1], v2 = rp[2], v3 = rp[3], v4 = rp[4], v5 = rp[5];
+    L.l1[0] = v0.x; L.l1[1] = v0.y; L.l1[2] = v0.z; L.l1[3] = v0.w;
+    L.l1[4] = v1.x; L.l1[5] = v1.y; L.l1[6] = v1.z; L.l1[7] = v1.w;
+    L.l2[0] = v2.x; L.l2[1] = v2.y; L.l2[2] = v2.z; L.l2[3] = v2.w;
+    L.l2[4] = v3.x; L.l2[5] = v3.y; L.l2[6] = v3.z; L.l2[7] = v3.w;
+    L.l3[0] = v4.x; L.l3[1] = v4.y; L.l3[2] = v4.z; L.l3[3] = v4.w;
+    L.l3[4] = v5.x; L.l3[5] = v5.y; L.l3[6] = v5.z; L.l3[7] = v5.w;
+    const float4 t = reinterpret_cast<const float4*>(lds + RECB * u)[6];
+    L.s1 = t.x;
+    L.S[0] = t.y;
+    L.S[1] = t.z;
+    L.S[2] = t.w;
+    L.S[3] = reinterpret_cast<const float*>(lds + RECB * u)[28];
+}
+
+}  // namespace fq

@@ -108,3 +108,53 @@ def dequantize_weight(b: QWeight) -> torch.Tensor:
 
 def row_bytes(dtype: int, K: int) -> int:
     return fmt(dtype).row_bytes(K)
+
+
+@dataclass
+class PackedWeight:
+    """A block-quantized weight in the aligned device layout (fq_pack_weights).
+
+    Same logical [N, K] matrix and identical dequantized values as the GGUF
+    bytes it was made from; rows are packed_row_bytes(K) apart.
+    """
+    data: torch.Tensor  # uint8, 16-byte aligned, on the device
+    dtype: int
+    N: int
+    K: int
+
+
+def packed_row_bytes(dtype: int, K: int) -> int:
+    return int(_lib.lib().fq_packed_row_bytes(int(dtype), int(K)))
+
+
+def pack_weights(b: QWeight) -> PackedWeight:
+    rb = packed_row_bytes(b.dtype, b.K)
+    if rb == 0:
+        raise RuntimeError(f"no packed layout for dtype {b.dtype} with K={b.K}")
+    out = torch.empty(b.N * rb, dtype=torch.uint8, device=b.data.device)
+    _lib.check(_lib.lib().fq_pack_weights(b.dtype, b.data.data_ptr(), out.data_ptr(), b.N, b.K,
+                                          _stream_ptr(b.data)), "fq_pack_weights")
+    return PackedWeight(out, b.dtype, b.N, b.K)
+
+
+def unpack_weights(p: PackedWeight) -> QWeight:
+    out = torch.empty(fmt(p.dtype).matrix_bytes(p.N, p.K), dtype=torch.uint8,
+                      device=p.data.device)
+    _lib.check(_lib.lib().fq_unpack_weights(p.dtype, p.data.data_ptr(), out.data_ptr(), p.N, p.K,
+                                            _stream_ptr(p.data)), "fq_unpack_weights")
+    return QWeight(out, p.dtype, p.N, p.K)
+
+
+def gemv_packed(x: torch.Tensor, p: PackedWeight, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Batch-1 GEMV over packed weights (x: [K] or [1, K]); returns [N]."""
+    xv = x.reshape(-1)
+    if xv.numel() != p.K:
+        raise RuntimeError(f"gemv_packed dimension mismatch: K={xv.numel()} K2={p.K}")
+    y = torch.empty((p.N,), dtype=torch.float32, device=x.device)
+    bptr, blen = None, 0
+    if bias is not None:
+        bias = bias.to(device=x.device, dtype=torch.float32).contiguous()
+        bptr, blen = bias.data_ptr(), bias.numel()
+    _lib.check(_lib.lib().fq_gemv_packed(p.dtype, xv.data_ptr(), p.data.data_ptr(), bptr, blen,
+                                         y.data_ptr(), p.K, p.N, _stream_ptr(x)), "fq_gemv_packed")
+    return y

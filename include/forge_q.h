@@ -42,6 +42,7 @@ extern "C" {
 #define FQ_ERR_NULL 3     /* a required pointer is NULL                           */
 #define FQ_ERR_HIP 4      /* the HIP runtime reported an error (fq_last_hip_error) */
 #define FQ_ERR_NO_DEVICE 5
+#define FQ_ERR_ALIGN 6     /* a packed-layout pointer is not 16-byte aligned       */
 
 /* DataType values accepted by the entry points. */
 #define FQ_DTYPE_Q4_0 2u
@@ -101,6 +102,35 @@ int fq_matmul_transB(uint32_t dtype, const float* x, const void* w, const float*
  * (cuda_quant.cu:131-335) and backs ops::dequantize_weight
  * (matmul.cpp:980-1003). */
 int fq_dequant_rows(uint32_t dtype, const void* w, float* out, int N, int K, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Aligned device layout ("packed").  GGUF blocks are 18/20/34/210 bytes, so
+ * most of them are only 2-byte aligned in memory.  The packed layout holds
+ * the same bytes of each row, moved so that every quant payload is a
+ * 16-byte-aligned run followed by dense scale arrays (Q4_K is unchanged).
+ * Dequantized values are identical: fq_unpack_weights restores the GGUF
+ * bytes exactly.  Requires K % 256 == 0 and 16-byte-aligned packed buffers.
+ * No counterpart in the reference (it reads GGUF blocks in place); it backs
+ * the load-time repack a loader may do when it copies a tensor to the device
+ * (Tensor::to_device, src/core/tensor.cpp; GGUF mapping gguf_model.cpp:57-90).
+ * ---------------------------------------------------------------------- */
+
+/* Bytes per row in the packed layout; 0 if the dtype or K is unsupported. */
+int64_t fq_packed_row_bytes(uint32_t dtype, int K);
+
+/* GGUF rows -> packed rows (device to device, N rows of length K). */
+int fq_pack_weights(uint32_t dtype, const void* w_gguf, void* w_packed, int N, int K,
+                    void* stream);
+
+/* Packed rows -> GGUF rows, bit-exact inverse of fq_pack_weights. */
+int fq_unpack_weights(uint32_t dtype, const void* w_packed, void* w_gguf, int N, int K,
+                      void* stream);
+
+/* Batch-1 GEMV over packed weights: y[n] = sum_k x[k] dequant(w)[n][k] (+ bias[n]
+ * for n < bias_len when bias != NULL).  Same results as fq_gemv on the GGUF
+ * bytes, within the path's tolerance; deterministic. */
+int fq_gemv_packed(uint32_t dtype, const float* x, const void* w_packed, const float* bias,
+                   int64_t bias_len, float* y, int K, int N, void* stream);
 
 #ifdef __cplusplus
 }

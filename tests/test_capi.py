@@ -83,3 +83,15 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(ImportError):
         _lib.lib()
+
+
+def test_packed_row_bytes():
+    L = _lib.lib()
+    # same bytes as the GGUF row (plus at most 15 bytes of row padding)
+    for dt, f in F.FORMATS.items():
+        for K in (256, 2048, 3584, 18944):
+            pb = L.fq_packed_row_bytes(dt, K)
+            assert pb % 16 == 0
+            assert f.row_bytes(K) <= pb <= f.row_bytes(K) + 15
+    assert L.fq_packed_row_bytes(F.Q4_0, 96) == 0  # K must be a multiple of 256
+    assert L.fq_packed_row_bytes(5, 256) == 0
