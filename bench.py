@@ -4,13 +4,16 @@
 
 A step is one batch-1 decode pass over the Qwen2.5-7B Q4_K_M-style projection
 mix (benchmark config 2): gate and up (Q4_K 18944x3584), down (Q6_K
-3584x18944) and lm_head (Q6_K 152064x3584), each one fq_gemv call through
-the C ABI.  Weights are seeded synthetic blocks resident in HBM; two full
-copies (1.16 GB) alternate between steps so no step can be served from the
-256 MB Infinity Cache.  Prints ONE JSON line:
+3584x18944) and lm_head (Q6_K 152064x3584), each one fq_gemv_packed call
+through the C ABI (--layout gguf: fq_gemv on the unmodified GGUF bytes).
+Weights are seeded synthetic blocks, repacked once into the aligned device
+layout at load time (outside the timed region, as a loader does) and resident
+in HBM; two full copies (1.16 GB) alternate between steps so no step can be
+served from the 256 MB Infinity Cache.  Prints ONE JSON line:
   value      whole-step algorithmic HBM bytes / step time, in GB/s
   roofline   the dominant kernel (lm_head), algorithmic bytes per launch over
-             its average launch time (HIP events on the launch stream)
+             its average launch time (K launches back to back, HIP events on
+             the launch stream around them)
   cpu_baseline  the reference's own AVX2+OpenMP ops::matmul_transB (compiled
              from its sources into oracle/_ref) on the same step, on this
              host's cores.
@@ -52,6 +55,11 @@ def parse():
     p.add_argument("--configs", action="store_true", help="also time configs 0-4 (stderr)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--layout", choices=("packed", "gguf"), default="packed",
+                   help="device weight layout: aligned repack (default) or GGUF bytes")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="before the timed region, copy MIB MiB device-to-device three times "
+                        "(a plain copy kernel of known size for scaling HBM byte counters)")
     return p.parse_args()
 
 
@@ -99,8 +107,11 @@ def cpu_baseline(host_w, host_x, budget_s):
     }
 
 
-def time_config(name, dtype, N, K, M, reps=40, pool_bytes=600 << 20):
-    """Median per-call device time of one matmul shape over rotated copies."""
+def time_config(name, dtype, N, K, M, reps=20, pool_bytes=600 << 20, packed=False):
+    """Average per-call device time of one matmul shape.  `reps` calls over
+    rotated weight copies (>= 600 MB, so calls stream from HBM) are captured
+    in one HIP graph, so host launch cost does not hide small kernels; the
+    graph is replayed and timed with events on its stream."""
     import torch
     from forge_amd import ops, synth
     nb = alg_bytes(dtype, N, K, M) - 4 * M * K - 4 * M * N
@@ -108,26 +119,50 @@ def time_config(name, dtype, N, K, M, reps=40, pool_bytes=600 << 20):
     w_np = synth.make_weights(dtype, N, K, seed=N + K)
     base = torch.from_numpy(w_np.reshape(-1)).cuda()
     ws = [ops.QWeight(base if i == 0 else base.clone(), dtype, N, K) for i in range(copies)]
+    if packed:
+        ws = [ops.pack_weights(w) for w in ws]
     x = torch.from_numpy(synth.make_x(M, K, 1)).cuda()
-    for i in range(copies):
-        ops.matmul_transB(x, ws[i])
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    from forge_amd import _lib
+    L = _lib.lib()
+
+    def call(w, stream):
+        if packed:
+            st = L.fq_gemv_packed(dtype, x.data_ptr(), w.data.data_ptr(), None, 0, y.data_ptr(),
+                                  K, N, stream)
+        else:
+            st = L.fq_matmul_transB(dtype, x.data_ptr(), w.data.data_ptr(), None, 0, 0,
+                                    y.data_ptr(), M, K, N, stream)
+        if st != 0:
+            raise RuntimeError(f"fq_matmul_transB failed with status {st} on {name}")
+
+    cur = torch.cuda.current_stream().cuda_stream
+    for i in range(copies):  # warm-up; grows the library workspace before capture
+        call(ws[i], cur)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(reps)]
-    for r in range(reps):
-        ev[r][0].record()
-        ops.matmul_transB(x, ws[r % copies])
-        ev[r][1].record()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gs = torch.cuda.current_stream().cuda_stream
+        for r in range(reps):
+            call(ws[r % copies], gs)
+    g.replay()
     torch.cuda.synchronize()
-    us = statistics.median(a.elapsed_time(b) * 1e3 for a, b in ev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (3 * reps)
     b = alg_bytes(dtype, N, K, M)
-    line = {"config": name, "M": M, "N": N, "K": K, "us": round(us, 2),
+    line = {"config": name, "layout": "packed" if packed else "gguf", "M": M, "N": N, "K": K,
+            "us": round(us, 2),
             "GBs": round(b / us / 1e3, 1), "pct_hbm": round(100 * b / us / 1e3 / PEAK_HBM_GBS, 1)}
     if M > 32:
         tf = 2.0 * M * N * K / us / 1e6
         line["TFLOPs"] = round(tf, 1)
         line["pct_fp16_mfma"] = round(100 * tf / PEAK_FP16_TFLOPS, 2)
-    del ws, base
+    del g, ws, base
     torch.cuda.empty_cache()
     return line
 
@@ -151,10 +186,14 @@ def main():
     # ---- inputs: seeded blocks, two device copies of the whole step
     host_w = [synth.make_weights(dt, N, K, seed=2000 + i) for i, (_, dt, N, K) in enumerate(CFG2)]
     host_x = {K: synth.make_x(1, K, seed=2100 + K) for K in {K for (_, _, _, K) in CFG2}}
+    packed = args.layout == "packed"
     sets = []
     for c in range(2):
-        sets.append([ops.QWeight(torch.from_numpy(w.reshape(-1)).cuda(), dt, N, K)
-                     for w, (_, dt, N, K) in zip(host_w, CFG2)])
+        ws = [ops.QWeight(torch.from_numpy(w.reshape(-1)).cuda(), dt, N, K)
+              for w, (_, dt, N, K) in zip(host_w, CFG2)]
+        sets.append([ops.pack_weights(w) for w in ws] if packed else ws)
+        del ws
+    torch.cuda.synchronize()
     xs = {K: torch.from_numpy(v).cuda() for K, v in host_x.items()}
     ys = [torch.empty((N,), dtype=torch.float32, device="cuda") for (_, _, N, _) in CFG2]
 
@@ -165,33 +204,53 @@ def main():
     def launch(i, s):
         (name, dt, N, K) = CFG2[i]
         w = sets[s][i]
-        st = L.fq_gemv(dt, xs[K].data_ptr(), w.data.data_ptr(), ys[i].data_ptr(), K, N, stream)
+        if packed:
+            st = L.fq_gemv_packed(dt, xs[K].data_ptr(), w.data.data_ptr(), None, 0,
+                                  ys[i].data_ptr(), K, N, stream)
+        else:
+            st = L.fq_gemv(dt, xs[K].data_ptr(), w.data.data_ptr(), ys[i].data_ptr(), K, N,
+                           stream)
         if st != 0:
-            raise RuntimeError(f"fq_gemv({name}) failed with status {st}")
+            raise RuntimeError(f"GEMV ({name}, {args.layout}) failed with status {st}")
 
     for s in range(args.warmup):
         for i in range(len(CFG2)):
             launch(i, s % 2)
     torch.cuda.synchronize()
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
-    # ---- timed region: K steps, HIP events around every launch
+    # ---- timed region: K steps launched back to back, HIP events on the
+    # launch stream around the whole region
     nk = len(CFG2)
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(nk)] for _ in range(args.steps)]
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record()
     for s in range(args.steps):
         for i in range(nk):
-            ev[s][i][0].record()
             launch(i, s % 2)
-            ev[s][i][1].record()
     t_end.record()
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
     ms_per_step = total_ms / args.steps
-    kern_us = [statistics.mean(ev[s][i][0].elapsed_time(ev[s][i][1]) * 1e3
-                               for s in range(args.steps)) for i in range(nk)]
+
+    # ---- per-kernel average launch time: each matrix alone, K launches back
+    # to back (alternating the two weight copies), events around the loop
+    kern_us = []
+    for i in range(nk):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        launch(i, 1)
+        e0.record()
+        for s in range(args.steps):
+            launch(i, s % 2)
+        e1.record()
+        torch.cuda.synchronize()
+        kern_us.append(e0.elapsed_time(e1) * 1e3 / args.steps)
 
     step_bytes = sum(alg_bytes(dt, N, K) for (_, dt, N, K) in CFG2)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
@@ -204,7 +263,8 @@ def main():
     lm = per_kernel["lm_head"]
     roofline = {"bound": "hbm", "achieved": lm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(lm["GBs"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
-                "kernel": "gemv_kernel<Q6_K> (lm_head 152064x3584, M=1)",
+                "kernel": ("gemvp_kernel<Q6_K>" if packed else "gemv1r_kernel<Q6_K>")
+                + " (lm_head 152064x3584, M=1)",
                 "alg_bytes_per_launch": lm["alg_bytes"]}
 
     cpu = None
@@ -227,7 +287,7 @@ def main():
         "config": {"workload": "cfg2: Qwen2.5-7B Q4_K_M decode projections at M=1 "
                                "(gate,up Q4_K 18944x3584; down Q6_K 3584x18944; "
                                "lm_head Q6_K 152064x3584)",
-                   "M": 1, "step_alg_bytes": step_bytes,
+                   "M": 1, "layout": args.layout, "step_alg_bytes": step_bytes,
                    "pct_hbm_peak": round(100 * value / PEAK_HBM_GBS, 1),
                    "per_kernel": per_kernel},
         "roofline": roofline,
@@ -242,27 +302,31 @@ def main():
 
 def measured_traffic():
     """HBM bytes per lm_head launch from the committed rocprofv3 --pmc runs
-    (profiles/lm_head_q6k_traffic.json), or None when not measured."""
-    path = os.path.join(ROOT, "profiles", "lm_head_q6k_traffic.json")
-    if not os.path.exists(path):
-        return None
+    (the JSON block of profiles/lm_head_q6k_traffic.md), or None when not
+    measured."""
+    path = os.path.join(ROOT, "profiles", "lm_head_q6k_traffic.md")
     try:
-        with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
+        text = open(path).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block).get("hbm_bytes_per_launch")
+    except (OSError, ValueError, IndexError):
         return None
 
 
 def all_configs():
     Q4_0, Q8_0, Q4_K, Q6_K = 2, 7, 4, 13
-    lines = [time_config("cfg0", Q4_0, 5632, 2048, 1)]
-    for dt in (Q4_0, Q8_0):
-        for n, N, K in [("q", 2048, 2048), ("k", 256, 2048), ("v", 256, 2048), ("o", 2048, 2048),
-                        ("gate", 5632, 2048), ("up", 5632, 2048), ("down", 2048, 5632)]:
-            lines.append(time_config(f"cfg1-{n}-{'q4_0' if dt == Q4_0 else 'q8_0'}", dt, N, K, 1))
-    for n, dt, N, K in [("gate", Q4_K, 18944, 3584), ("down", Q6_K, 3584, 18944),
-                        ("lm_head", Q6_K, 152064, 3584)]:
-        lines.append(time_config(f"cfg2-{n}", dt, N, K, 1))
+    lines = []
+    for pk in (False, True):
+        lines.append(time_config("cfg0", Q4_0, 5632, 2048, 1, packed=pk))
+        for dt in (Q4_0, Q8_0):
+            for n, N, K in [("q", 2048, 2048), ("k", 256, 2048), ("o", 2048, 2048),
+                            ("gate", 5632, 2048), ("down", 2048, 5632)]:
+                lines.append(time_config(f"cfg1-{n}-{'q4_0' if dt == Q4_0 else 'q8_0'}", dt, N,
+                                         K, 1, packed=pk))
+        for n, dt, N, K in [("gate", Q4_K, 18944, 3584), ("down", Q6_K, 3584, 18944),
+                            ("lm_head", Q6_K, 152064, 3584)]:
+            lines.append(time_config(f"cfg2-{n}", dt, N, K, 1, packed=pk))
+    lines.append(time_config("cfg3", Q4_K, 14336, 4096, 1, packed=True))
     for M in (1, 2, 4, 8, 16):
         lines.append(time_config("cfg3", Q4_K, 14336, 4096, M))
     for dt in (Q8_0, Q4_0):

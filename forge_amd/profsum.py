@@ -1,0 +1,104 @@
+"""Summarise a rocprofv3 kernel trace per kernel launch shape.
+
+    python -m forge_amd.profsum <prefix>_kernel_trace.csv [--title TEXT]
+    python -m forge_amd.profsum --traffic FETCH.csv WRITE.csv --copy-mib MIB \
+        --kernel NAME_PREFIX --grid G --lds B
+
+rocprofv3's own ``--stats`` table averages every launch of one kernel symbol,
+but one template instance serves several matrices (the Q6_K GEMV runs both
+down 3584x18944 and lm_head 152064x3584).  This groups the dispatches by
+(kernel, grid, work-group, LDS bytes) instead -- LDS bytes follow the row
+length K -- and prints a Markdown table of calls and durations in µs.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import statistics
+
+
+def summarise(path: str):
+    groups = collections.OrderedDict()
+    for r in csv.DictReader(open(path)):
+        key = (r["Kernel_Name"], int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]),
+               int(r["LDS_Block_Size"]), int(r["VGPR_Count"]), int(r["Scratch_Size"]))
+        groups.setdefault(key, []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    rows = []
+    for (name, grid, wg, lds, vgpr, scratch), d in groups.items():
+        rows.append({"kernel": name, "grid": grid, "wg": wg, "lds": lds, "vgpr": vgpr,
+                     "scratch": scratch, "calls": len(d), "avg_us": statistics.mean(d),
+                     "median_us": statistics.median(d), "min_us": min(d), "max_us": max(d)})
+    rows.sort(key=lambda r: -r["avg_us"] * r["calls"])
+    return rows
+
+
+def short(name: str) -> str:
+    name = name.replace("fq::(anonymous namespace)::", "").replace("void ", "")
+    return name.split("(")[0] if "(" in name else name
+
+
+def counter_groups(path: str):
+    """Mean counter value per (kernel, grid, LDS bytes) of a --pmc CSV."""
+    g = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        g[(short(r["Kernel_Name"]), int(r["Grid_Size"]), int(r["LDS_Block_Size"]))].append(
+            float(r["Counter_Value"]))
+    return {k: statistics.mean(v) for k, v in g.items()}
+
+
+def traffic(fetch_csv, write_csv, copy_mib, kernel, grid, lds):
+    """HBM bytes per launch of one kernel shape from FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch), each scaled by what the same counter reads for the
+    plain device-to-device copy of copy_mib MiB that ran in the same process
+    (it reads and writes copy_mib MiB)."""
+    f, w = counter_groups(fetch_csv), counter_groups(write_csv)
+    kib = copy_mib * 1024.0
+
+    def copy_val(groups):
+        vals = [v for (n, _, _), v in groups.items() if "copyBuffer" in n or "copy" in n.lower()]
+        best = max(vals)  # the calibration copy is by far the largest copy
+        return best
+
+    cf, cw = copy_val(f) / kib, copy_val(w) / kib
+    key = [k for k in f if k[0].startswith(kernel) and k[1] == grid and k[2] == lds]
+    if len(key) != 1:
+        raise SystemExit(f"kernel shape not found uniquely: {key}")
+    k = key[0]
+    fetch_b = f[k] * 1024.0 / cf
+    write_b = w[k] * 1024.0 / cw
+    return {"kernel": k[0], "grid": grid, "lds": lds,
+            "fetch_kib_raw": round(f[k], 1), "write_kib_raw": round(w[k], 1),
+            "fetch_scale": round(cf, 5), "write_scale": round(cw, 5),
+            "fetch_bytes": int(fetch_b), "write_bytes": int(write_b),
+            "hbm_bytes_per_launch": int(fetch_b + write_b)}
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("trace", nargs="?")
+    p.add_argument("--title", default="")
+    p.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    p.add_argument("--copy-mib", type=float, default=448)
+    p.add_argument("--kernel", default="gemvp_kernel<13")
+    p.add_argument("--grid", type=int, default=0)
+    p.add_argument("--lds", type=int, default=0)
+    a = p.parse_args()
+    if a.traffic:
+        import json
+        print(json.dumps(traffic(a.traffic[0], a.traffic[1], a.copy_mib, a.kernel, a.grid,
+                                 a.lds), indent=1))
+        return
+    if a.title:
+        print(f"# {a.title}\n")
+    print("| kernel | grid | wg | LDS B | VGPR | scratch | calls | avg µs | median µs | min µs | max µs |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for r in summarise(a.trace):
+        print(f"| `{short(r['kernel'])}` | {r['grid']} | {r['wg']} | {r['lds']} | {r['vgpr']} | "
+              f"{r['scratch']} | {r['calls']} | {r['avg_us']:.2f} | {r['median_us']:.2f} | "
+              f"{r['min_us']:.2f} | {r['max_us']:.2f} |")
+
+
+if __name__ == "__main__":
+    main()
