@@ -136,15 +136,17 @@ def time_config(name, dtype, N, K, M, reps=20, pool_bytes=600 << 20, packed=Fals
         if st != 0:
             raise RuntimeError(f"fq_matmul_transB failed with status {st} on {name}")
 
-    cur = torch.cuda.current_stream().cuda_stream
-    for i in range(copies):  # warm-up; grows the library workspace before capture
-        call(ws[i], cur)
+    # the library keeps its scratch per stream: warm up on the capture stream
+    # so nothing is allocated while capturing
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    for i in range(copies):
+        call(ws[i], side.cuda_stream)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        gs = torch.cuda.current_stream().cuda_stream
+    with torch.cuda.graph(g, stream=side):
         for r in range(reps):
-            call(ws[r % copies], gs)
+            call(ws[r % copies], side.cuda_stream)
     g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

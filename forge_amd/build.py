@@ -21,7 +21,8 @@ OBJDIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["fq_gemv.hip", "fq_gemv1.hip", "fq_gemvp.hip", "fq_pack.hip", "fq_mmq.hip", "fq_capi.cpp"]
+SOURCES = ["fq_dequant.hip", "fq_gemv1.hip", "fq_gemvp.hip", "fq_pack.hip", "fq_mmq.hip",
+           "fq_capi.cpp"]
 
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",

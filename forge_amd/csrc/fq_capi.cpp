@@ -1,9 +1,11 @@
 // fq_capi.cpp -- the extern "C" entry points declared in include/forge_q.h:
-// argument validation, launch planning and the split-K workspace.
+// argument validation, launch planning and the per-stream scratch memory.
 //
-// The planner mirrors the reference's dispatch on M (matmul.cpp:1150-1286:
-// M == 1 -> GEMV, 1 < M <= 32 -> batched GEMV, M > 32 -> prefill) and picks,
-// per call, how many K-splits and persistent work-groups fill the chip.
+// M == 1 runs the batch-1 GEMV kernels (fq_gemv1.hip on GGUF bytes,
+// fq_gemvp.hip on the aligned layout); every M > 1 -- the reference's
+// batched GEMV (1 < M <= 32) and its dequant + GEMM prefill (M > 32),
+// matmul.cpp:1150-1286 -- runs the MFMA kernels of fq_mmq.hip, which pick
+// their tile shape from M.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -65,96 +67,77 @@ DevInfo device_info(int dev) {
     return d;
 }
 
-// Split-K workspace: one grow-only pair of buffers per (device, stream) --
-// partial sums and arrival counters -- kept until process exit, so calls on
-// different streams never share one.  Counters are zeroed when allocated and
-// every call leaves them zero again.
-struct Workspace {
-    float* part = nullptr;
-    size_t part_bytes = 0;
-    unsigned* cnt = nullptr;
-    size_t cnt_words = 0;
-};
-
-hipError_t workspace(int dev, hipStream_t st, size_t part_bytes, size_t cnt_words, int grid,
-                     float** part, unsigned** cnt) {
+// Grow-only device scratch per (device, stream) for the MFMA path: token
+// operands, group sums, exponents and split-K partial slabs.
+hipError_t scratch(int dev, hipStream_t st, size_t bytes, uint8_t** out) {
     static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, Workspace> bufs;
+    static std::map<std::pair<int, hipStream_t>, std::pair<uint8_t*, size_t>> bufs;
     std::lock_guard<std::mutex> lk(mu);
-    Workspace& w = bufs[{dev, st}];
-    hipError_t err = hipSuccess;
-    if (w.part_bytes < part_bytes || w.cnt_words < cnt_words) {
-        // the old buffers may still be in use by queued work on this stream
-        if (w.part || w.cnt) {
-            err = hipStreamSynchronize(st);
-            if (err != hipSuccess) return err;
+    auto& b = bufs[{dev, st}];
+    if (b.second < bytes) {
+        if (b.first) {
+            hipError_t e = hipStreamSynchronize(st);  // queued work may still read it
+            if (e != hipSuccess) return e;
+            hipFree(b.first);
+            b.first = nullptr;
+            b.second = 0;
         }
-        if (w.part_bytes < part_bytes) {
-            if (w.part) hipFree(w.part);
-            w.part = nullptr;
-            w.part_bytes = 0;
-            err = hipMalloc(reinterpret_cast<void**>(&w.part), part_bytes);
-            if (err != hipSuccess) return err;
-            w.part_bytes = part_bytes;
-        }
-        if (w.cnt_words < cnt_words) {
-            if (w.cnt) hipFree(w.cnt);
-            w.cnt = nullptr;
-            w.cnt_words = 0;
-            err = hipMalloc(reinterpret_cast<void**>(&w.cnt), cnt_words * sizeof(unsigned));
-            if (err != hipSuccess) return err;
-            w.cnt_words = cnt_words;
-            err = fq::launch_zero(w.cnt, cnt_words, grid, st);
-            if (err != hipSuccess) return err;
-        }
+        hipError_t e = hipMalloc(reinterpret_cast<void**>(&b.first), bytes);
+        if (e != hipSuccess) return e;
+        b.second = bytes;
     }
-    *part = w.part;
-    *cnt = w.cnt;
+    *out = b.first;
     return hipSuccess;
 }
 
-constexpr int kWG = 256;
-constexpr int kT = 16;
-constexpr int kRowsPerWG = 16;
-constexpr int kMaxNU = 8;
-
-// Plan a launch of gemv_kernel for M tokens processed MT at a time: as few
-// K-splits as keep every lane at <= 8 units per row (more only when there are
-// fewer row groups than CUs), then enough persistent work-groups to fill the
-// chip once.
-int plan(uint32_t dtype, const Geometry& g, int M, int K, int N, int MT, const DevInfo& di,
-         fq::LaunchCfg& c, int& U, int& Uc) {
-    (void)g;
-    U = K / 32;
-    const long RG = (N + kRowsPerWG - 1) / kRowsPerWG;
-    const int TG = (M + MT - 1) / MT;
-    int S = std::max(1, (U + kMaxNU * kT - 1) / (kMaxNU * kT));
-    while (RG * S * TG < di.cus && (U + S) / (S + 1) >= 2 * kT) ++S;
-    auto lds_of = [&](int uc) { return (size_t)MT * uc * 36 * sizeof(float); };
-    const size_t lds_cap = std::min<size_t>(di.lds, 160 * 1024);
-    while (lds_of((U + S - 1) / S) > lds_cap) ++S;
-    Uc = U > 0 ? (U + S - 1) / S : 0;
-    S = U > 0 ? (U + Uc - 1) / Uc : 1;
-    const int nu = (Uc + kT - 1) / kT;
-    c.T = kT;
-    c.MT = MT;
-    c.NU = nu <= 2 ? 2 : nu <= 4 ? 4 : 8;
-    c.splits = S;
-    c.token_groups = TG;
-    c.lds_bytes = lds_of(Uc);
-    const void* fn = fq::gemv_kernel_fn((int)dtype, kT, MT, c.NU);
-    if (!fn) return FQ_ERR_DTYPE;
-    int per_cu = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWG, c.lds_bytes);
+// M > 1 on the matrix cores: token operand preparation, then one tile per
+// work-group (K-split when the tiles alone do not fill the chip).
+int run_mmq(uint32_t dtype, const Geometry& g, const float* x, const void* w, const float* bias,
+            int bias_mode, int64_t bias_len, float* y, int M, int K, int N, int dev,
+            const DevInfo& di, hipStream_t st) {
+    const int Tp = (M + 15) / 16, NC = (K + 63) / 64;
+    const int shape = Tp == 1 ? fq::MMQ_SMALL1 : Tp == 2 ? fq::MMQ_SMALL2
+                      : Tp <= 4 ? fq::MMQ_MID : fq::MMQ_BIG;
+    int bn = 0, bm = 0;
+    fq::mmq_shape(shape, &bn, &bm);
+    const int gx = (N + bn - 1) / bn, gy = (Tp + bm / 16 - 1) / (bm / 16);
+    const long tiles = (long)gx * gy;
+    int splits = (int)std::max(1L, std::min<long>((2L * di.cus + tiles - 1) / tiles, 8));
+    splits = std::max(1, std::min(splits, NC / 4));
+    const size_t xop_b = (size_t)Tp * NC * 2048 * 2, xsum_b = (size_t)Tp * NC * 64 * 4,
+                 ex_b = (size_t)Tp * NC * 16 * 4;
+    const size_t part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    uint8_t* buf = nullptr;
+    hipError_t e = scratch(dev, st, 256 + al(xop_b) + al(xsum_b) + al(ex_b) + al(part_b), &buf);
     if (e != hipSuccess) return hip_fail(e);
-    if (per_cu < 1) per_cu = 1;
-    const long gx = (long)di.cus * per_cu / ((long)S * TG);
-    c.grid_x = (int)std::max(1L, std::min(RG, gx));
-    return FQ_OK;
+    fq::MmqArgs a{};
+    a.w = static_cast<const uint8_t*>(w);
+    a.xop = buf;
+    a.xsum = reinterpret_cast<const float*>(buf + al(xop_b));
+    a.ex = reinterpret_cast<const int*>(buf + al(xop_b) + al(xsum_b));
+    a.part = splits > 1 ? reinterpret_cast<float*>(buf + al(xop_b) + al(xsum_b) + al(ex_b))
+                        : nullptr;
+    a.y = y;
+    a.bias = bias;
+    a.bias_len = bias_mode ? bias_len : 0;
+    a.bias_mode = bias_mode;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.NC = NC;
+    a.row_bytes = (K / g.be) * g.bb;
+    if (NC > 0) {  // K == 0 only writes the bias (or zeros)
+        e = fq::launch_xprep((int)dtype, x, M, K, NC, reinterpret_cast<_Float16*>(buf),
+                             const_cast<float*>(a.xsum), const_cast<int*>(a.ex), st);
+        if (e != hipSuccess) return hip_fail(e);
+    }
+    e = fq::launch_mmq((int)dtype, a, shape, gx, gy, splits, st);
+    return e == hipSuccess ? FQ_OK : hip_fail(e);
 }
 
 int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias, int bias_mode,
-               int64_t bias_len, float* y, int M, int K, int N, int MT, hipStream_t st) {
+               int64_t bias_len, float* y, int M, int K, int N, hipStream_t st) {
     Geometry g;
     if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
     if (M < 0 || N < 0 || K < 0) return FQ_ERR_SHAPE;
@@ -177,20 +160,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     if (M == 1 && K > 0) {
         // batch 1: persistent work-groups, as many as fit on every CU
         const int U1 = K / 32;
-        static const int wg_env = [] {
-            const char* v = getenv("FQ_GEMV1_WG");
-            return v ? atoi(v) : 1024;
-        }();
-        int wg = wg_env;
+        int wg = 1024;
         size_t lds = fq::gemv1_lds_bytes((int)dtype, U1, wg);
         const void* fn = fq::gemv1_kernel_fn((int)dtype, bias_mode != 0, wg);
-        static const bool no_rowstep = getenv("FQ_NO_ROWSTEP") != nullptr;
         int npr = 0;
         size_t lds_r = 0;
         int wg_r = 0;
-        const void* fr = no_rowstep ? nullptr
-                                    : fq::gemv1r_kernel_fn((int)dtype, U1, (K / g.be) * g.bb,
-                                                           bias_mode != 0, &npr, &lds_r, &wg_r);
+        const void* fr = fq::gemv1r_kernel_fn((int)dtype, U1, (K / g.be) * g.bb, bias_mode != 0,
+                                              &npr, &lds_r, &wg_r);
         if (fr && lds_r <= std::min<size_t>(di.lds, 160 * 1024)) {
             fn = fr;
             lds = lds_r;
@@ -224,41 +201,8 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         }
     }
 
-    fq::LaunchCfg c{};
-    int U = 0, Uc = 0;
-    int rc = plan(dtype, g, M, K, N, MT, di, c, U, Uc);
-    if (rc != FQ_OK) return rc;
-
-    fq::GemvArgs a{};
-    a.x = x;
-    a.w = static_cast<const uint8_t*>(w);
-    a.y = y;
-    a.bias = bias;
-    a.bias_len = bias_len;
-    a.bias_mode = bias_mode;
-    a.M = M;
-    a.K = K;
-    a.N = N;
-    a.U = U;
-    a.Uc = std::max(Uc, 1);
-    a.row_bytes = (K / g.be) * g.bb;
-    a.rg_total = (N + kRowsPerWG - 1) / kRowsPerWG;
-    a.part = nullptr;
-    a.counters = nullptr;
-    if (c.splits > 1) {
-        e = workspace(dev, st, sizeof(float) * (size_t)c.splits * M * N,
-                      (size_t)c.token_groups * a.rg_total, di.cus, &a.part, &a.counters);
-        if (e != hipSuccess) return hip_fail(e);
-    }
-    e = fq::launch_gemv((int)dtype, a, c, st);
-    if (e != hipSuccess) return hip_fail(e);
-    return FQ_OK;
-}
-
-int pick_mt(int M) {
-    if (M <= 1) return 1;
-    if (M == 2) return 2;
-    return 4;
+    // M > 1, and M == 1 rows too long for the batch-1 kernels' LDS
+    return run_mmq(dtype, g, x, w, bias, bias_mode, bias_len, y, M, K, N, dev, di, st);
 }
 
 }  // namespace
@@ -289,21 +233,21 @@ const char* fq_status_str(int status) {
 int fq_last_hip_error(void) { return g_last_hip; }
 
 int fq_gemv(uint32_t dtype, const float* x, const void* w, float* y, int K, int N, void* stream) {
-    return run_matmul(dtype, x, w, nullptr, 0, 0, y, 1, K, N, 1,
+    return run_matmul(dtype, x, w, nullptr, 0, 0, y, 1, K, N,
                       static_cast<hipStream_t>(stream));
 }
 
 int fq_gemv_batch(uint32_t dtype, const float* x, const void* w, float* y, int M, int K, int N,
                   void* stream) {
     if (M < 1 || M > 32) return FQ_ERR_SHAPE;
-    return run_matmul(dtype, x, w, nullptr, 0, 0, y, M, K, N, pick_mt(M),
+    return run_matmul(dtype, x, w, nullptr, 0, 0, y, M, K, N,
                       static_cast<hipStream_t>(stream));
 }
 
 int fq_matmul_prefill(uint32_t dtype, const float* x, const void* w, float* y, int M, int K,
                       int N, void* stream) {
     if (M < 1) return FQ_ERR_SHAPE;
-    return run_matmul(dtype, x, w, nullptr, 0, 0, y, M, K, N, pick_mt(M),
+    return run_matmul(dtype, x, w, nullptr, 0, 0, y, M, K, N,
                       static_cast<hipStream_t>(stream));
 }
 
@@ -314,7 +258,7 @@ int fq_matmul_transB(uint32_t dtype, const float* x, const void* w, const float*
     if (bias && bias_ndim == 1) mode = 1;
     else if (bias && bias_ndim == 2) mode = 2;
     else if (bias && bias_ndim != 0) return FQ_ERR_SHAPE;
-    return run_matmul(dtype, x, w, bias, mode, bias_len, y, M, K, N, pick_mt(M),
+    return run_matmul(dtype, x, w, bias, mode, bias_len, y, M, K, N,
                       static_cast<hipStream_t>(stream));
 }
 

@@ -1,0 +1,63 @@
+// fq_dequant.hip -- the bit-exact dequant kernel (fq_dequant_rows) and a
+// small fill kernel used instead of memset nodes, so callers may capture it.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fq_formats.h"
+#include "fq_kernels.h"
+
+namespace fq {
+
+// Dequantize: one thread per (row, unit), bit-identical to the reference's
+// row routines (scalar fp16 conversion, reference expression order).
+template <int F>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ w,
+                                                      float* __restrict__ out, int N, int K,
+                                                      int U, int row_bytes) {
+    using Fm = Fmt<F>;
+    constexpr int NG = Fm::NG, GS = 32 / NG;
+    const size_t total = (size_t)N * U;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * 256) {
+        const int row = (int)(i / U), u = (int)(i - (size_t)row * U);
+        const uint8_t* wr = w + (size_t)row * row_bytes;
+        float q[32], A[NG], B[NG];
+        Fm::template decode<true>(Fm::load(wr, u), u, q, A, B);
+        float* o = out + (size_t)row * K;
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+            const int k = Fm::k_of(u, s);
+            if (k < K) o[k] = Fm::value(q[s], A[s / GS], B[s / GS]);
+        }
+    }
+}
+
+// Clears n words.
+__global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        p[i] = 0u;
+}
+
+hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st) {
+    hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(256), 0, st, p, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,
+                          int row_bytes, int grid, hipStream_t st) {
+#define FQ_DQ(F)                                                                              \
+    hipLaunchKernelGGL(dequant_kernel<F>, dim3(grid), dim3(256), 0, st, w, out, N, K, U,      \
+                       row_bytes);                                                            \
+    return hipGetLastError();
+    switch (dtype) {
+        case Q4_0: FQ_DQ(Q4_0)
+        case Q4_1: FQ_DQ(Q4_1)
+        case Q8_0: FQ_DQ(Q8_0)
+        case Q4_K: FQ_DQ(Q4_K)
+        case Q6_K: FQ_DQ(Q6_K)
+        default: return hipErrorInvalidValue;
+    }
+#undef FQ_DQ
+}
+
+}  // namespace fq

@@ -1,5 +1,5 @@
 // fq_kernels.h -- launch interface between the C ABI (fq_capi.cpp) and the
-// HIP kernels (fq_gemv.hip, fq_mmq.hip).  Internal to the library.
+// HIP kernels.  Internal to the library.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,9 +11,6 @@ struct GemvArgs {
     const float* x;       // [M][K]
     const uint8_t* w;     // [N] rows of row_bytes
     float* y;             // [M][N]
-    float* part;          // [splits][M][N] when splits > 1, else nullptr
-    unsigned* counters;   // [token_groups][rg_total] split arrival counters (zero between calls)
-    int rg_total;         // row groups of 16 rows: ceil(N / 16)
     const float* bias;    // optional, see bias_mode
     int64_t bias_len;
     int bias_mode;        // 0 none, 1 row vector over n, 2 full [M][N]
@@ -21,22 +18,8 @@ struct GemvArgs {
     int U;                // 32-weight units per row (K / 32)
     int Uc;               // units per K-split
     int row_bytes;
-    int split_units;      // packed split-K: lane units per K-slice
-    int waves_total;      // packed split-K: counter stride (waves in the grid)
 };
 
-struct LaunchCfg {
-    int T;                // lanes per row (16)
-    int MT;               // tokens per work-group: 1, 2 or 4
-    int NU;               // max units per lane per row: 2, 4 or 8
-    int grid_x;           // persistent work-groups per (split, token group)
-    int splits;           // grid.y
-    int token_groups;     // grid.z
-    size_t lds_bytes;
-};
-
-hipError_t launch_gemv(int dtype, const GemvArgs& a, const LaunchCfg& c, hipStream_t st);
-const void* gemv_kernel_fn(int dtype, int T, int MT, int NU);
 // batch-1 persistent kernel (fq_gemv1.hip)
 const void* gemv1_kernel_fn(int dtype, bool bias, int wg);
 size_t gemv1_lds_bytes(int dtype, int U, int wg);
@@ -51,6 +34,25 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
 hipError_t launch_pack(int dtype, const uint8_t* src, uint8_t* dst, int N, int K, bool pack,
                        int grid, hipStream_t st);
 hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st);
+// M > 1 on MFMA (fq_mmq.hip)
+struct MmqArgs {
+    const uint8_t* w;     // GGUF rows
+    const void* xop;      // fp16 token operands, [Tp][NC][2048]
+    const float* xsum;    // [Tp][NC][64] sub-block sums of the scaled activations
+    const int* ex;        // [Tp][NC][16] power-of-two exponent per (token, chunk)
+    float* y;             // [M][N]
+    float* part;          // [splits][M][N] when splits > 1
+    const float* bias;
+    int64_t bias_len;
+    int bias_mode;
+    int M, N, K, NC, row_bytes;
+};
+enum { MMQ_SMALL1 = 0, MMQ_SMALL2 = 1, MMQ_MID = 2, MMQ_BIG = 3 };
+void mmq_shape(int shape, int* bn, int* bm);
+hipError_t launch_xprep(int dtype, const float* x, int M, int K, int NC, _Float16* xop,
+                        float* xsum, int* ex, hipStream_t st);
+hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, int splits,
+                      hipStream_t st);
 hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,
                           int row_bytes, int grid, hipStream_t st);
 
