@@ -56,8 +56,8 @@ struct Pk<Q8_0> {
     using Raw = Fmt<Q8_0>::Raw;
     __device__ static int k_of(int w, int s) { return 32 * w + s; }
     __device__ static Raw load(const uint8_t* row, int v, int U) {
-        return Raw{ldg16<true>(row + 32 * U + 2 * v), ldg128<true>(row + 32 * v),
-                   ldg128<true>(row + 32 * v + 16)};
+        return Raw{ldg16<true>(row + 32 * U + 2 * v), ldg128<true>(row + 16 * v),
+                   ldg128<true>(row + 16 * U + 16 * v)};
     }
     __device__ static float dot(const Raw& r, int v, const Limbs* L) {
         return limb_dot<Q8_0>(r, v, L[0]);
@@ -72,14 +72,13 @@ struct Q4KP {
 };
 
 template <>
-struct Pk<Q4_K> {  // the GGUF super-block is already 16-byte aligned
+struct Pk<Q4_K> {  // planes q0, q1 (U x 16 each), then the headers (S x 16)
     static constexpr int NREC = 2, NG = 1;
     using Raw = Q4KP;
     __device__ static int k_of(int w, int s) { return 32 * w + s; }
-    __device__ static Raw load(const uint8_t* row, int v, int) {
-        const uint8_t* sb = row + 144 * (v >> 2);
-        const uint8_t* q = sb + 16 + 32 * (v & 3);
-        return Raw{ldg128<true>(sb), ldg128<true>(q), ldg128<true>(q + 16)};
+    __device__ static Raw load(const uint8_t* row, int v, int U) {
+        return Raw{ldg128<true>(row + 32 * U + 16 * (v >> 2)), ldg128<true>(row + 16 * v),
+                   ldg128<true>(row + 16 * U + 16 * v)};
     }
     __device__ static float dot(const Raw& r, int v, const Limbs* L) {
         const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
@@ -126,8 +125,8 @@ struct Pk<Q6_K> {
     // U here = lane units per row = K / 64; super-blocks S = U / 4.
     __device__ static Raw load(const uint8_t* row, int v, int U) {
         const int S = U >> 2, sb = v >> 2, n = (v & 3) >> 1;
-        const uint8_t* pay = row + 48 * v;
-        return Raw{ldg128<true>(pay), ldg128<true>(pay + 16), ldg128<true>(pay + 32),
+        return Raw{ldg128<true>(row + 16 * v), ldg128<true>(row + 16 * U + 16 * v),
+                   ldg128<true>(row + 32 * U + 16 * v),
                    ldg64<true>(row + 192 * S + 16 * sb + 8 * n),
                    ldg16<true>(row + 208 * S + 2 * sb)};
     }

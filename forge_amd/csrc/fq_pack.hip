@@ -47,20 +47,28 @@ __global__ __launch_bounds__(256) void pack_kernel(int dtype, uint8_t* raw, uint
                 move<PACK>(rr + 20 * b, pr + 16 * U + 4 * b, 4);
                 break;
             case 7:  // Q8_0: d | qs[32]
-                move<PACK>(rr + 34 * b + 2, pr + 32 * b, 32);
+                move<PACK>(rr + 34 * b + 2, pr + 16 * b, 16);
+                move<PACK>(rr + 34 * b + 18, pr + 16 * U + 16 * b, 16);
                 move<PACK>(rr + 34 * b, pr + 32 * U + 2 * b, 2);
                 break;
-            case 4:  // Q4_K: identical
-                move<PACK>(rr + 144 * b, pr + 144 * b, 144);
+            case 4: {  // Q4_K: d dmin scales[12] | qs[128]
+                const int V = K / 64;
+                uint8_t* sb = rr + 144 * b;
+                for (int g = 0; g < 4; ++g) {
+                    move<PACK>(sb + 16 + 32 * g, pr + 16 * (4 * b + g), 16);
+                    move<PACK>(sb + 32 + 32 * g, pr + 16 * V + 16 * (4 * b + g), 16);
+                }
+                move<PACK>(sb, pr + 32 * V + 16 * b, 16);
                 break;
+            }
             case 13: {  // Q6_K: ql[128] qh[64] sc[16] d
+                const int V = K / 64;
                 uint8_t* sb = rr + 210 * b;
-                uint8_t* pay = pr + 192 * b;
                 for (int p = 0; p < 4; ++p) {
-                    const int n = p >> 1, h = p & 1;
-                    move<PACK>(sb + 64 * n + 16 * h, pay + 48 * p, 16);
-                    move<PACK>(sb + 64 * n + 32 + 16 * h, pay + 48 * p + 16, 16);
-                    move<PACK>(sb + 128 + 32 * n + 16 * h, pay + 48 * p + 32, 16);
+                    const int n = p >> 1, h = p & 1, v = 4 * b + p;
+                    move<PACK>(sb + 64 * n + 16 * h, pr + 16 * v, 16);
+                    move<PACK>(sb + 64 * n + 32 + 16 * h, pr + 16 * V + 16 * v, 16);
+                    move<PACK>(sb + 128 + 32 * n + 16 * h, pr + 32 * V + 16 * v, 16);
                 }
                 move<PACK>(sb + 192, pr + 192 * S + 16 * b, 16);
                 move<PACK>(sb + 208, pr + 208 * S + 2 * b, 2);
