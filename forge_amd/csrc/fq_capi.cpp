@@ -347,11 +347,13 @@ int fq_gemv_packed(uint32_t dtype, const float* x, const void* w_packed, const f
     if (e != hipSuccess) return hip_fail(e);
     if (per_cu < 1) return FQ_ERR_SHAPE;
     const int wpb = wg / 64;
-    // one work-group per resident slot, each owning a contiguous row range of
-    // at most 4096 rows (its LDS result buffer) and at least one row per wave
+    // one work-group per resident slot, each owning a contiguous row range
+    // with at least one row per wave, and whose row x K-slice partial sums fit
+    // its 4096-entry LDS buffer (slices of 64 lane units)
+    const long ns = (units + 63) / 64;
     long G = (long)di.cus * per_cu;
     G = std::max(1L, std::min<long>(G, ((long)N + wpb - 1) / wpb));
-    G = std::max<long>(G, ((long)N + 4095) / 4096);
+    G = std::max<long>(G, ((long)N * ns + 4095) / 4096);
     fq::GemvArgs a{};
     a.x = x;
     a.w = static_cast<const uint8_t*>(w_packed);

@@ -175,50 +175,58 @@ struct Pk<Q6_K> {
     }
 };
 
-// Work distribution.  Work-group g owns the contiguous rows [N g / G,
-// N (g+1) / G); within it, waves claim chunks of CR rows through an LDS
+// Work distribution.  Work-group g owns the contiguous rows [lo, hi) =
+// [N g / G, N (g+1) / G).  Its work is the sequence of (K-slice, row) steps
+// in slice-major order, f = s * rows + r (a K-slice is 64 lane units), cut
+// into items of CR consecutive steps.  Waves claim items in order from an LDS
 // counter, so a wave that the SIMD arbiter serves less often simply takes
-// fewer chunks (static striding left waves of one CU finishing up to 20%
-// apart).  A chunk is processed slice-major: for each K-slice of 64*NL lane
-// units, the slice's activation limbs are loaded into registers and that
-// slice of every row of the chunk is accumulated into the row's lane of the
-// result register; slices are added in slice order, so the result is
-// deterministic.  Finished chunk results go to an LDS row buffer that the
-// work-group writes to y, coalesced, when its rows are done: the pipelined
-// loop issues no global stores and no global atomics.
-constexpr int CR = 2;          // rows per claimed chunk (at least)
-constexpr int YBUF = 4096;     // rows of results a work-group buffers in LDS
-
-struct Chunk {
-    int r0, n;  // first row, rows (0: no more work)
-};
+// fewer items, and rows with many slices (long K, few rows) still spread over
+// every wave.  A wave reloads its activation limbs only when its slice
+// changes.  The row sum of step f goes to the LDS buffer part[f]; at the end
+// the work-group adds the slices of each row in slice order (so the result
+// does not depend on which wave took which item) and writes y coalesced.
+// The pipelined loop issues no global stores and no global atomics.
+constexpr int CR = 3;          // steps per item; an item spans >= D steps
+constexpr int YBUF = 4096;     // row x slice partial sums a work-group buffers in LDS
 
 struct It {
-    int r0, n, s, r;  // chunk, slice, row within chunk
+    int f0, n, k, s, r;  // item [f0, f0 + n), step k of it = (slice s, row r)
 };
 
-// Uniform claim of the next chunk from the work-group's LDS counter.
-__device__ __forceinline__ Chunk claim(int* ctr, int hi, int cr, int lane) {
-    int r0 = 0;
-    if (lane == 0) r0 = atomicAdd(ctr, cr);
-    r0 = __builtin_amdgcn_readfirstlane(r0);
-    return Chunk{r0, r0 < hi ? min(cr, hi - r0) : 0};
+struct Claims {
+    int* ctr;
+    int total, rows;
+};
+
+// Uniform claim of the next item from the work-group's LDS counter.
+__device__ __forceinline__ It claim(const Claims& cl, int lane) {
+    int i = 0;
+    if (lane == 0) i = atomicAdd(cl.ctr, 1);
+    i = __builtin_amdgcn_readfirstlane(i);
+    const int f0 = i * CR;
+    if (f0 >= cl.total) return It{0, 0, 0, 0, 0};
+    const int s = f0 / cl.rows;
+    return It{f0, min(CR, cl.total - f0), 0, s, f0 - s * cl.rows};
 }
 
-// The chunk the load side has claimed beyond the compute side's chunk (n = 0:
-// none).  A chunk spans at least D steps (the host picks CR so) and only a
-// work-group's last chunk is shorter, so the load side, D steps ahead, is at
-// most one chunk ahead and one slot suffices.  Uniform scalars only: an
-// indexed queue would live in scratch memory, whose loads share the in-order
-// vector memory counter with the weight loads and drain them.
-struct Next {
-    int r0, n;
-};
+// The item the load side has claimed beyond the compute side's item (n = 0:
+// none).  Every item but the last spans CR >= D steps, so the load side, D
+// steps ahead, is at most one item ahead and one slot suffices.  Uniform
+// scalars only: an indexed queue would live in scratch memory, whose loads
+// share the in-order vector memory counter with the weight loads and drain
+// them.
+__device__ __forceinline__ void next_step(It& t, int rows) {
+    ++t.k;
+    if (++t.r == rows) {
+        t.r = 0;
+        ++t.s;
+    }
+}
 
 template <int F, int NL>
 __device__ __forceinline__ void pload(typename Pk<F>::Raw (&f)[NL], const GemvArgs& a,
-                                      const It& t, int lane) {
-    const uint8_t* r = a.w + (size_t)min(t.r0 + t.r, a.N - 1) * a.row_bytes;
+                                      const It& t, int lo, int lane) {
+    const uint8_t* r = a.w + (size_t)min(lo + t.r, a.N - 1) * a.row_bytes;
     const int v0 = t.s * 64 * NL;
 #pragma unroll
     for (int c = 0; c < NL; ++c) f[c] = Pk<F>::load(r, min(v0 + lane + 64 * c, a.U - 1), a.U);
@@ -234,30 +242,27 @@ __device__ __forceinline__ void load_slice_limbs(Limbs (&L)[NL][Pk<F>::NREC], co
             read_limbs(L[c][r], lds, min(s * 64 * NL + lane + 64 * c, U - 1) * Pk<F>::NREC + r);
 }
 
-__device__ __forceinline__ void advance_load(It& ld, Next& q, int ns, int cr, int* ctr, int hi,
-                                             int lane) {
+__device__ __forceinline__ void advance_load(It& ld, It& q, const Claims& cl, int lane) {
     if (ld.n == 0) return;
-    if (++ld.r == ld.n) {
-        ld.r = 0;
-        if (++ld.s == ns) {
-            ld.s = 0;
-            const Chunk c = claim(ctr, hi, cr, lane);
-            ld.r0 = c.r0;
-            ld.n = c.n;
-            if (c.n > 0) q = Next{c.r0, c.n};
-        }
+    next_step(ld, cl.rows);
+    if (ld.k == ld.n) {
+        ld = claim(cl, lane);
+        if (ld.n > 0) q = ld;
     }
 }
 
-// One step of the compute side (slice cp.s of row cp.r0 + cp.r), then the
-// loads of the load side's step into the same registers.
+// One step of the compute side (slice cp.s of row lo + cp.r), then the loads
+// of the load side's step into the same registers.
 template <int F, int NL, int D, bool BIAS>
-__device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& ld, Next& q,
-                                      int ns, int cr, int* ctr, int hi, const GemvArgs& a,
+__device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& ld, It& q,
+                                      const Claims& cl, const GemvArgs& a,
                                       Limbs (&L)[NL][Pk<F>::NREC], const uint8_t* lds,
-                                      float* ybuf, int lo, int lane, float& res) {
+                                      float* part, int lo, int lane, int& cur_s, float& res) {
     __builtin_amdgcn_sched_barrier(0);
-    if (cp.r == 0) load_slice_limbs<F, NL>(L, lds, cp.s, a.U, lane);  // wave-uniform
+    if (cp.s != cur_s) {  // wave-uniform
+        load_slice_limbs<F, NL>(L, lds, cp.s, a.U, lane);
+        cur_s = cp.s;
+    }
     const int v0 = cp.s * 64 * NL;
     float acc = 0.0f;
 #pragma unroll
@@ -266,78 +271,78 @@ __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& 
         const float t = Pk<F>::dot(f[c], min(v, a.U - 1), L[c]);
         acc += v < a.U ? t : 0.0f;
     }
-    pload<F, NL>(f, a, ld, lane);
+    pload<F, NL>(f, a, ld, lo, lane);
     float s = __builtin_bit_cast(
         float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
     if constexpr (BIAS) {
         if (cp.s == 0) {
-            const int r = cp.r0 + cp.r;
+            const int r = lo + cp.r;
             s += r < a.bias_len ? ((const_fp)(uintptr_t)a.bias)[r] : 0.0f;
         }
     }
-    res = lane == cp.r ? res + s : res;
-    // advance the compute side; a finished chunk goes to the LDS row buffer
-    if (++cp.r == cp.n) {
-        cp.r = 0;
-        if (++cp.s == ns) {
-            cp.s = 0;
-            if (lane < cp.n) ybuf[cp.r0 - lo + lane] = res;
-            res = 0.0f;
-            cp.r0 = q.r0;
-            cp.n = q.n;
-            q.n = 0;
-        }
+    res = lane == cp.k ? res + s : res;
+    // advance the compute side; a finished item goes to the LDS partial buffer
+    next_step(cp, cl.rows);
+    if (cp.k == cp.n) {
+        if (lane < cp.n) part[cp.f0 + lane] = res;
+        res = 0.0f;
+        cp = q;
+        q.n = 0;
     }
-    // after the compute side has taken the pending chunk, so the slot is free
-    advance_load(ld, q, ns, cr, ctr, hi, lane);
+    // after the compute side has taken the pending item, so the slot is free
+    advance_load(ld, q, cl, lane);
     __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int F, int NL, int D, bool BIAS, int WG>
 __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
+    static_assert(D <= CR, "an item must span at least D steps");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int ctr;
-    __shared__ float ybuf[YBUF];
+    __shared__ float part[YBUF];
     using P = Pk<F>;
     const int lane = threadIdx.x & 63;
     const int ns = (a.U + 64 * NL - 1) / (64 * NL);
     const int G = gridDim.x, g = blockIdx.x;
-    const int lo_all = (int)((int64_t)a.N * g / G), hi_all = (int)((int64_t)a.N * (g + 1) / G);
+    // the host sizes the grid so (hi - lo) * ns <= YBUF
+    const int lo = (int)((int64_t)a.N * g / G), hi = (int)((int64_t)a.N * (g + 1) / G);
+    const int rows = hi - lo;
+    const Claims cl{&ctr, rows * ns, rows};
 
-    // the host sizes the grid so a work-group owns at most YBUF rows
-    const int lo = lo_all, hi = hi_all;
-    if (threadIdx.x == 0) ctr = lo;
+    if (threadIdx.x == 0) ctr = 0;
     XStage<P, WG> xs;
     stage_load<P, WG>(xs, a.x, a.Uc, 0);  // activation loads before any weight load
     __syncthreads();
     // the first D steps' weight loads; the limb records are built while they
     // are in flight
-    const int cr = max(CR, (D + ns - 1) / ns);  // a chunk spans >= D steps
-    Next q{0, 0};
-    const Chunk c0 = claim(&ctr, hi, cr, lane);
-    It ld{c0.r0, c0.n, 0, 0}, cp{c0.r0, c0.n, 0, 0};
+    It q{0, 0, 0, 0, 0};
+    It ld = claim(cl, lane), cp = ld;
     typename P::Raw f[D][NL];
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-        pload<F, NL>(f[j], a, ld, lane);
-        advance_load(ld, q, ns, cr, &ctr, hi, lane);
+        pload<F, NL>(f[j], a, ld, lo, lane);
+        advance_load(ld, q, cl, lane);
     }
     stage_build<P, WG>(lds, xs, a.x, a.Uc, 0);
     Limbs L[NL][P::NREC];
     float res = 0.0f;
+    int cur_s = -1;
     while (cp.n > 0) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
             if (cp.n > 0)
-                pstep<F, NL, D, BIAS>(f[j], cp, ld, q, ns, cr, &ctr, hi, a, L, lds, ybuf, lo, lane,
-                                      res);
+                pstep<F, NL, D, BIAS>(f[j], cp, ld, q, cl, a, L, lds, part, lo, lane, cur_s, res);
         }
     }
     __syncthreads();
-    for (int r = threadIdx.x; r < hi - lo; r += WG) a.y[lo + r] = ybuf[r];
+    for (int r = threadIdx.x; r < rows; r += WG) {
+        float v = part[r];
+        for (int s = 1; s < ns; ++s) v += part[s * rows + r];
+        a.y[lo + r] = v;
+    }
 }
 
-constexpr int WGP = 512;
+constexpr int WGP = 1024;
 constexpr int DP = 3;
 
 template <int F, int NL>
@@ -347,8 +352,8 @@ const void* pfn2(bool bias) {
 }
 
 template <int F>
-const void* pfn(int nl, bool bias) {
-    return nl == 1 ? pfn2<F, 1>(bias) : pfn2<F, 2>(bias);
+const void* pfn(bool bias) {
+    return pfn2<F, 1>(bias);
 }
 
 }  // namespace
@@ -364,19 +369,16 @@ void gemvp_geometry(int dtype, int K, int* units, int* records) {
     }
 }
 
-// Kernel for a row of `units` lane units: K-slices of 64 units (one per lane)
-// or, for the 32-weight units of long rows, of 128 (two per lane).
+// Kernel for a row of `units` lane units: K-slices of 64 units (one per lane).
 const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg) {
-    // 64-weight lane units (Q4_K, Q6_K) keep one unit per lane: two would
-    // need ~230 registers and halve the resident waves
-    const int nl = (units <= 64 || dtype == Q4_K || dtype == Q6_K) ? 1 : 2;
+    (void)units;
     const void* fn = nullptr;
     switch (dtype) {
-        case Q4_0: fn = pfn<Q4_0>(nl, bias); break;
-        case Q4_1: fn = pfn<Q4_1>(nl, bias); break;
-        case Q8_0: fn = pfn<Q8_0>(nl, bias); break;
-        case Q4_K: fn = pfn<Q4_K>(nl, bias); break;
-        case Q6_K: fn = pfn<Q6_K>(nl, bias); break;
+        case Q4_0: fn = pfn<Q4_0>(bias); break;
+        case Q4_1: fn = pfn<Q4_1>(bias); break;
+        case Q8_0: fn = pfn<Q8_0>(bias); break;
+        case Q4_K: fn = pfn<Q4_K>(bias); break;
+        case Q6_K: fn = pfn<Q6_K>(bias); break;
     }
     *lds = (size_t)records * RECB;
     *wg = WGP;
