@@ -57,6 +57,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--layout", choices=("packed", "gguf"), default="packed",
                    help="device weight layout: aligned repack (default) or GGUF bytes")
+    p.add_argument("--graph", action="store_true",
+                   help="replay each step as one captured HIP graph instead of four launches")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="before the timed region, copy MIB MiB device-to-device three times "
                         "(a plain copy kernel of known size for scaling HBM byte counters)")
@@ -201,7 +203,10 @@ def main():
 
     from forge_amd import _lib
     L = _lib.lib()
-    stream = torch.cuda.current_stream().cuda_stream
+    # every launch goes to one side stream, which is also the capture stream
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    stream = side.cuda_stream
 
     def launch(i, s):
         (name, dt, N, K) = CFG2[i]
@@ -227,16 +232,32 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    # ---- timed region: K steps launched back to back, HIP events on the
-    # launch stream around the whole region
+    # ---- timed region: K steps, HIP events on the launch stream around the
+    # whole region.  The step's four kernels are launched one by one; --graph
+    # replays each step as one captured HIP graph instead (measured no faster
+    # on MI355X for these launch sizes).
     nk = len(CFG2)
+    graphs = []
+    if args.graph:
+        for c in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for i in range(nk):
+                    launch(i, c)
+            graphs.append(g)
+        for g in graphs:
+            g.replay()
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t_start.record()
-    for s in range(args.steps):
-        for i in range(nk):
-            launch(i, s % 2)
-    t_end.record()
+    with torch.cuda.stream(side):
+        t_start.record()
+        for s in range(args.steps):
+            if graphs:
+                graphs[s % 2].replay()
+            else:
+                for i in range(nk):
+                    launch(i, s % 2)
+        t_end.record()
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
     ms_per_step = total_ms / args.steps
@@ -247,10 +268,11 @@ def main():
     for i in range(nk):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         launch(i, 1)
-        e0.record()
-        for s in range(args.steps):
-            launch(i, s % 2)
-        e1.record()
+        with torch.cuda.stream(side):
+            e0.record()
+            for s in range(args.steps):
+                launch(i, s % 2)
+            e1.record()
         torch.cuda.synchronize()
         kern_us.append(e0.elapsed_time(e1) * 1e3 / args.steps)
 
@@ -289,7 +311,9 @@ def main():
         "config": {"workload": "cfg2: Qwen2.5-7B Q4_K_M decode projections at M=1 "
                                "(gate,up Q4_K 18944x3584; down Q6_K 3584x18944; "
                                "lm_head Q6_K 152064x3584)",
-                   "M": 1, "layout": args.layout, "step_alg_bytes": step_bytes,
+                   "M": 1, "layout": args.layout,
+                   "launch": "hip_graph" if args.graph else "stream",
+                   "step_alg_bytes": step_bytes,
                    "pct_hbm_peak": round(100 * value / PEAK_HBM_GBS, 1),
                    "per_kernel": per_kernel},
         "roofline": roofline,

@@ -309,12 +309,15 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     const int rows = hi - lo;
     const Claims cl{&ctr, rows * ns, rows};
 
+    // limb records first, so the activation loads never queue behind the
+    // weight stream; then the first D steps of weight loads
     if (threadIdx.x == 0) ctr = 0;
-    XStage<P, WG> xs;
-    stage_load<P, WG>(xs, a.x, a.Uc, 0);  // activation loads before any weight load
+    {
+        XStage<P, WG> xs;
+        stage_load<P, WG>(xs, a.x, a.Uc, 0);
+        stage_build<P, WG, false>(lds, xs, a.x, a.Uc, 0);
+    }
     __syncthreads();
-    // the first D steps' weight loads; the limb records are built while they
-    // are in flight
     It q{0, 0, 0, 0, 0};
     It ld = claim(cl, lane), cp = ld;
     typename P::Raw f[D][NL];
@@ -323,7 +326,6 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
         pload<F, NL>(f[j], a, ld, lo, lane);
         advance_load(ld, q, cl, lane);
     }
-    stage_build<P, WG>(lds, xs, a.x, a.Uc, 0);
     Limbs L[NL][P::NREC];
     float res = 0.0f;
     int cur_s = -1;

@@ -54,7 +54,8 @@ __device__ __forceinline__ void stage_load(XStage<Fm, WG>& st, const float* __re
     const int tasks = 8 * nrec;
 #pragma unroll
     for (int p = 0; p < XPMAX; ++p)
-        st.v[p] = stage_x4<Fm>(x, w0, min(p * WG + (int)threadIdx.x, tasks - 1));
+        if (p * WG < tasks)  // uniform
+            st.v[p] = stage_x4<Fm>(x, w0, min(p * WG + (int)threadIdx.x, tasks - 1));
 }
 
 template <int CTRL>
@@ -121,7 +122,7 @@ __device__ __forceinline__ void build_task(uint8_t* lds, float4 xv, int t, int t
     }
 }
 
-template <class Fm, int WG>
+template <class Fm, int WG, bool SYNC = true>
 __device__ __forceinline__ void stage_build(uint8_t* lds, const XStage<Fm, WG>& st,
                                             const float* __restrict__ x, int nrec, int w0) {
     const int tasks = 8 * nrec;
@@ -134,7 +135,7 @@ __device__ __forceinline__ void stage_build(uint8_t* lds, const XStage<Fm, WG>& 
         const int t = base + (int)threadIdx.x;
         build_task<Fm>(lds, stage_x4<Fm>(x, w0, min(t, tasks - 1)), t, tasks);
     }
-    __syncthreads();
+    if (SYNC) __syncthreads();
 }
 
 // One-call form for kernels with nothing to overlap.
