@@ -280,14 +280,16 @@ __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& 
             s += r < a.bias_len ? ((const_fp)(uintptr_t)a.bias)[r] : 0.0f;
         }
     }
-    res = lane == cp.k ? res + s : res;
     // advance the compute side; a finished item goes to the LDS partial buffer
-    next_step(cp, cl.rows);
-    if (cp.k == cp.n) {
-        if (lane < cp.n) part[cp.f0 + lane] = res;
-        res = 0.0f;
-        cp = q;
-        q.n = 0;
+    if (cp.n > 0) {  // wave-uniform; past the last item the step only keeps the loads in step
+        res = lane == cp.k ? res + s : res;
+        next_step(cp, cl.rows);
+        if (cp.k == cp.n) {
+            if (lane < cp.n) part[cp.f0 + lane] = res;
+            res = 0.0f;
+            cp = q;
+            q.n = 0;
+        }
     }
     // after the compute side has taken the pending item, so the slot is free
     advance_load(ld, q, cl, lane);
@@ -329,12 +331,14 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     Limbs L[NL][P::NREC];
     float res = 0.0f;
     int cur_s = -1;
+    // every iteration runs all D steps, each issuing its loads, so the number
+    // of loads in flight at the loop head is always the same and the compiler
+    // waits for exactly one step's loads (a skipped step would make it drain
+    // the whole queue)
     while (cp.n > 0) {
 #pragma unroll
-        for (int j = 0; j < D; ++j) {
-            if (cp.n > 0)
-                pstep<F, NL, D, BIAS>(f[j], cp, ld, q, cl, a, L, lds, part, lo, lane, cur_s, res);
-        }
+        for (int j = 0; j < D; ++j)
+            pstep<F, NL, D, BIAS>(f[j], cp, ld, q, cl, a, L, lds, part, lo, lane, cur_s, res);
     }
     __syncthreads();
     for (int r = threadIdx.x; r < rows; r += WG) {

@@ -12,8 +12,9 @@
 // so the block scales never touch fp16.  y = 2^e_m acc at the end.
 //
 // Two kernels:
-//  xprep_kernel  one work-group per token: e_m, x_hi/x_lo in MFMA operand
-//                order (chunks of KC = 64 elements), the group sums S.
+//  xprep_kernel  one work-group per (16 tokens, chunk of KC = 64 elements):
+//                per-(token, chunk) exponents, x_hi/x_lo in MFMA operand
+//                order, the sub-block sums S.
 //  mmq_kernel    one work-group per (BN rows x BM tokens x K-split) tile:
 //                per chunk it stages the token operands (a straight copy) and
 //                the weight tile (decoded to fp16 quants plus A, B per
@@ -66,64 +67,50 @@ struct SubBlock {
 // group g = (kl % SB) / EPL, is slot e' (slot_elem(e') = kl % EPL) of
 //   xop[(t NC + ch) XOP + s 2 BLK + hl BLK + (16 g + c) EPL + e']
 // and xsum[(t NC + ch) XSUM + s 16 + c] is the sum of x 2^-e over sub-block s.
-// Work-group: 16 tokens x 4 chunks; thread (c, q, p) handles the 16 elements
-// [16 p, 16 p + 16) of chunk 4 blockIdx.y + q of token c.
+// Work-group (t, ch): 16 tokens x 64 elements; thread (c, p) handles the
+// aligned quad [4 p, 4 p + 4) of token c (slot_elem permutes within quads).
 template <int SB>
 __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int M, int K,
                                                     int NC, _Float16* __restrict__ xop,
                                                     float* __restrict__ xsum, int* __restrict__ ex) {
     using G = Geo<SB>;
     constexpr int EPL = G::EPL;
-    const int c = threadIdx.x >> 4, q = (threadIdx.x >> 2) & 3, p = threadIdx.x & 3;
-    const int t = blockIdx.x, m = 16 * t + c, ch = 4 * blockIdx.y + q;
-    if (ch >= NC) return;  // whole groups of four lanes leave together
-    const int k0 = ch * KC + 16 * p;
-    const bool live = m < M && k0 < K;  // K is a multiple of 32
+    const int c = threadIdx.x >> 4, p = threadIdx.x & 15;
+    const int t = blockIdx.x, ch = blockIdx.y, m = 16 * t + c;
+    const int k0 = ch * KC + 4 * p;
+    const bool live = m < M && k0 < K;  // K is a multiple of 32: quads are all in or all out
     const float* xr = x + (size_t)min(m, M - 1) * K + (live ? k0 : 0);
-    float v[16];
+    float v[4];
     float mx = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < 4; ++i) {
         v[i] = live ? xr[i] : 0.0f;
         mx = fmaxf(mx, fabsf(v[i]));
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     int e = 0;
     if (mx > 0.0f && mx <= 3.0e38f) e = ilogbf(mx) - 14;
     const size_t blk = (size_t)t * NC + ch;
     if (p == 0) ex[blk * 16 + c] = e;
-    float sum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        v[i] = ldexpf(v[i], -e);
-        sum += v[i];
+    for (int i = 0; i < 4; ++i) v[i] = ldexpf(v[i], -e);
+    const int kl = 4 * p, s = kl / SB, g = (kl % SB) / EPL;
+    _Float16* dst = xop + blk * XOP + s * 2 * G::BLK + (16 * g + c) * EPL + (kl % EPL);
+    h4 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float w = v[slot_elem(i)];
+        hi[i] = (_Float16)w;
+        lo[i] = (_Float16)(w - (float)hi[i]);
     }
-    _Float16* base = xop + blk * XOP;
+    *reinterpret_cast<h4*>(dst) = hi;
+    *reinterpret_cast<h4*>(dst + G::BLK) = lo;
+    // sub-block sums: a fixed tree over the SB / 4 threads of the sub-block
+    float sum = (v[0] + v[1]) + (v[2] + v[3]);
 #pragma unroll
-    for (int gg = 0; gg < 16 / EPL; ++gg) {  // EPL-element groups of this thread
-        const int kl = 16 * p + EPL * gg;
-        const int s = kl / SB, g = (kl % SB) / EPL;
-        _Float16* dst = base + s * 2 * G::BLK + (16 * g + c) * EPL;
-        _Float16 hi[EPL], lo[EPL];
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-            const float w = v[EPL * gg + slot_elem(i)];
-            hi[i] = (_Float16)w;
-            lo[i] = (_Float16)(w - (float)hi[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-            dst[i] = hi[i];
-            dst[G::BLK + i] = lo[i];
-        }
-    }
-    if constexpr (SB == 32) {  // two threads per sub-block: lower half first
-        const float o = __shfl_xor(sum, 1, 64);
-        if ((p & 1) == 0) xsum[blk * XSUM + (p >> 1) * 16 + c] = sum + o;
-    } else {
-        xsum[blk * XSUM + p * 16 + c] = sum;
-    }
+    for (int o = 1; o < SB / 4; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    if ((p % (SB / 4)) == 0) xsum[blk * XSUM + s * 16 + c] = sum;
 }
 
 // ------------------------------------------------------------ weight decode
@@ -551,7 +538,7 @@ void mmq_shape(int shape, int* bn, int* bm) {
 
 hipError_t launch_xprep(int dtype, const float* x, int M, int K, int NC, _Float16* xop,
                         float* xsum, int* ex, hipStream_t st) {
-    const dim3 grid((M + 15) / 16, (NC + 3) / 4);
+    const dim3 grid((M + 15) / 16, NC);
     if (dtype == Q6_K)
         hipLaunchKernelGGL(xprep_kernel<16>, grid, dim3(256), 0, st, x, M, K, NC, xop, xsum, ex);
     else
