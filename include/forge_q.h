@@ -106,8 +106,9 @@ int fq_dequant_rows(uint32_t dtype, const void* w, float* out, int N, int K, voi
 /* ------------------------------------------------------------------------
  * Aligned device layout ("packed").  GGUF blocks are 18/20/34/210 bytes, so
  * most of them are only 2-byte aligned in memory.  The packed layout holds
- * the same bytes of each row, moved so that every quant payload is a
- * 16-byte-aligned run followed by dense scale arrays (Q4_K is unchanged).
+ * the same bytes of each row, moved into 16-byte-aligned "planes" (the piece
+ * a GEMV lane reads for lane unit v sits at plane + 16 v) followed by dense
+ * scale arrays; the per-format layout is documented in forge_amd/csrc/fq_pack.h.
  * Dequantized values are identical: fq_unpack_weights restores the GGUF
  * bytes exactly.  Requires K % 256 == 0 and 16-byte-aligned packed buffers.
  * No counterpart in the reference (it reads GGUF blocks in place); it backs
