@@ -350,6 +350,13 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
 __device__ __forceinline__ float limb_sum(int d1, int d2, int d3) {
     return __builtin_fmaf((float)d3, 0x1p-14f, __builtin_fmaf((float)d2, 0x1p-7f, (float)d1));
 }
+
+// The same sum times 2^14 for 4-bit quants, combined in integers first: with
+// q <= 15 each |d| <= 32 * 127 * 15, so d1 2^14 + d2 2^7 + d3 < 2^30 fits an
+// int32, and one conversion replaces three (rounding: 2^-24 relative).
+__device__ __forceinline__ float limb_sum4(int d1, int d2, int d3) {
+    return (float)((d1 << 14) + (d2 << 7) + d3);
+}
 // q dword holding slots 4i..4i+3 (bytes 0..127 as signed int8), group g
 template <int G>
 __device__ __forceinline__ void acc_dword(int q, int i, const Limbs& L, int (&D)[3][G], int g) {
@@ -380,7 +387,8 @@ __device__ __forceinline__ float limb_dot<Q4_0>(const Fmt<Q4_0>::Raw& r, int, co
     nibble_dots<1>(r.qs, L, D);
     const float d = f16_hw(r.d);
     // d * (sum x q) - 8 d * (sum x)
-    return __builtin_fmaf(d * L.s1, limb_sum(D[0][0], D[1][0], D[2][0]), -8.0f * d * L.S[0]);
+    return __builtin_fmaf(d * L.s1 * 0x1p-14f, limb_sum4(D[0][0], D[1][0], D[2][0]),
+                          -8.0f * d * L.S[0]);
 }
 
 template <>
@@ -388,7 +396,7 @@ __device__ __forceinline__ float limb_dot<Q4_1>(const Fmt<Q4_1>::Raw& r, int, co
     int D[3][1] = {{0}, {0}, {0}};
     nibble_dots<1>(r.qs, L, D);
     const float d = f16_hw(r.dm & 0xFFFFu), m = f16_hw(r.dm >> 16);
-    return __builtin_fmaf(d * L.s1, limb_sum(D[0][0], D[1][0], D[2][0]), m * L.S[0]);
+    return __builtin_fmaf(d * L.s1 * 0x1p-14f, limb_sum4(D[0][0], D[1][0], D[2][0]), m * L.S[0]);
 }
 
 template <>
@@ -407,11 +415,11 @@ __device__ __forceinline__ float limb_dot<Q4_K>(const Fmt<Q4_K>::Raw& r, int u, 
     const float d = f16_hw(r.hdr.x & 0xFFFFu), dmin = f16_hw(r.hdr.x >> 16);
     uint32_t sa, ma, sb, mb;
     Fmt<Q4_K>::scale_min(r.hdr, (u & 7) >> 1, sa, ma, sb, mb);
-    const float ds = d * L.s1;
+    const float ds = d * L.s1 * 0x1p-14f;
     float acc = -(dmin * (float)ma) * L.S[0];
     acc = __builtin_fmaf(-(dmin * (float)mb), L.S[1], acc);
-    acc = __builtin_fmaf(ds * (float)sa, limb_sum(D[0][0], D[1][0], D[2][0]), acc);
-    return __builtin_fmaf(ds * (float)sb, limb_sum(D[0][1], D[1][1], D[2][1]), acc);
+    acc = __builtin_fmaf(ds * (float)sa, limb_sum4(D[0][0], D[1][0], D[2][0]), acc);
+    return __builtin_fmaf(ds * (float)sb, limb_sum4(D[0][1], D[1][1], D[2][1]), acc);
 }
 
 template <>

@@ -96,10 +96,12 @@ struct Pk<Q4_K> {  // planes q0, q1 (U x 16 each), then the headers (S x 16)
         const float d = f16_hw(r.hdr.x & 0xFFFFu), dmin = f16_hw(r.hdr.x >> 16);
         uint32_t sa, ma, sb, mb;
         Fmt<Q4_K>::scale_min(r.hdr, v & 3, sa, ma, sb, mb);
+        const float d14 = d * 0x1p-14f;
         float acc = -(dmin * (float)ma) * L[0].S[0];
         acc = __builtin_fmaf(-(dmin * (float)mb), L[1].S[0], acc);
-        acc = __builtin_fmaf(d * (float)sa * L[0].s1, limb_sum(D[0][0], D[1][0], D[2][0]), acc);
-        return __builtin_fmaf(d * (float)sb * L[1].s1, limb_sum(D[0][1], D[1][1], D[2][1]), acc);
+        acc = __builtin_fmaf(d14 * (float)sa * L[0].s1, limb_sum4(D[0][0], D[1][0], D[2][0]), acc);
+        return __builtin_fmaf(d14 * (float)sb * L[1].s1, limb_sum4(D[0][1], D[1][1], D[2][1]),
+                              acc);
     }
 };
 
