@@ -339,6 +339,62 @@ def measured_traffic():
         return None
 
 
+def time_fused(name, dtype, N, K, reps=20, pool_bytes=600 << 20):
+    """Average device time of the fused gate/up (fq_ffn_up_fused_packed, one
+    launch) next to the two separate packed GEMVs, both HIP-graph replays."""
+    import torch
+    from forge_amd import _lib, ops, synth
+    L = _lib.lib()
+    nb = 2 * (alg_bytes(dtype, N, K) - 4 * K - 4 * N)
+    copies = max(2, -(-pool_bytes // nb))
+    pairs = []
+    for c in range(copies):
+        g = ops.QWeight.from_numpy(synth.make_weights(dtype, N, K, seed=3 * c), dtype, N, K)
+        u = ops.QWeight.from_numpy(synth.make_weights(dtype, N, K, seed=3 * c + 1), dtype, N, K)
+        pairs.append((ops.pack_weights(g), ops.pack_weights(u)))
+        del g, u
+    x = torch.from_numpy(synth.make_x(1, K, 1)).cuda()
+    y = torch.empty(N, device="cuda")
+    y2 = torch.empty(N, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def fused(p, st):
+        assert L.fq_ffn_up_fused_packed(dtype, x.data_ptr(), p[0].data.data_ptr(),
+                                        p[1].data.data_ptr(), y.data_ptr(), K, N, st) == 0
+
+    def separate(p, st):
+        for w, out in ((p[0], y), (p[1], y2)):
+            assert L.fq_gemv_packed(dtype, x.data_ptr(), w.data.data_ptr(), None, 0,
+                                    out.data_ptr(), K, N, st) == 0
+
+    out = {"config": name, "M": 1, "N": N, "K": K, "op": "ffn_up_fused (gate+up+SiLU)"}
+    for label, fn in (("fused_us", fused), ("two_gemv_us", separate)):
+        for p in pairs:
+            fn(p, side.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            for r in range(reps):
+                fn(pairs[r % copies], side.cuda_stream)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out[label] = round(e0.elapsed_time(e1) * 1e3 / (3 * reps), 2)
+        del g
+    b = 2 * alg_bytes(dtype, N, K) - 4 * K
+    out["fused_GBs"] = round(b / out["fused_us"] / 1e3, 1)
+    out["fused_pct_hbm"] = round(100 * b / out["fused_us"] / 1e3 / PEAK_HBM_GBS, 1)
+    del pairs
+    torch.cuda.empty_cache()
+    return out
+
+
 def all_configs():
     Q4_0, Q8_0, Q4_K, Q6_K = 2, 7, 4, 13
     lines = []
@@ -352,6 +408,8 @@ def all_configs():
         for n, dt, N, K in [("gate", Q4_K, 18944, 3584), ("down", Q6_K, 3584, 18944),
                             ("lm_head", Q6_K, 152064, 3584)]:
             lines.append(time_config(f"cfg2-{n}", dt, N, K, 1, packed=pk))
+    lines.append(time_fused("cfg2-gate+up", Q4_K, 18944, 3584))
+    lines.append(time_fused("cfg1-gate+up-q4_0", Q4_0, 5632, 2048))
     lines.append(time_config("cfg3", Q4_K, 14336, 4096, 1, packed=True))
     for M in (1, 2, 4, 8, 16):
         lines.append(time_config("cfg3", Q4_K, 14336, 4096, M))

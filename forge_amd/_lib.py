@@ -38,6 +38,8 @@ SIGNATURES = {
     "fq_pack_weights": (_I, [_U, _P, _P, _I, _I, _P]),
     "fq_unpack_weights": (_I, [_U, _P, _P, _I, _I, _P]),
     "fq_gemv_packed": (_I, [_U, _P, _P, _P, _L, _P, _I, _I, _P]),
+    "fq_ffn_up_fused": (_I, [_U, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "fq_ffn_up_fused_packed": (_I, [_U, _P, _P, _P, _P, _I, _I, _P]),
 }
 
 _lib = None

@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdint>
 #include <map>
+#include <tuple>
 #include <mutex>
 #include <utility>
 
@@ -69,11 +70,12 @@ DevInfo device_info(int dev) {
 
 // Grow-only device scratch per (device, stream) for the MFMA path: token
 // operands, group sums, exponents and split-K partial slabs.
-hipError_t scratch(int dev, hipStream_t st, size_t bytes, uint8_t** out) {
+// slot 0: the MFMA path's operands; slot 1: the fused FFN's gate/up rows.
+hipError_t scratch(int dev, hipStream_t st, size_t bytes, uint8_t** out, int slot = 0) {
     static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, std::pair<uint8_t*, size_t>> bufs;
+    static std::map<std::tuple<int, hipStream_t, int>, std::pair<uint8_t*, size_t>> bufs;
     std::lock_guard<std::mutex> lk(mu);
-    auto& b = bufs[{dev, st}];
+    auto& b = bufs[{dev, st, slot}];
     if (b.second < bytes) {
         if (b.first) {
             hipError_t e = hipStreamSynchronize(st);  // queued work may still read it
@@ -205,6 +207,67 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     return run_mmq(dtype, g, x, w, bias, bias_mode, bias_len, y, M, K, N, dev, di, st);
 }
 
+// Batch-1 GEMV over packed rows; w2 != NULL: the fused gate/up form, y[n] =
+// silu(x . w[n]) * (x . w2[n]), run as one GEMV over 2 N interleaved rows.
+int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
+                const float* bias, int64_t bias_len, float* y, int K, int N, hipStream_t st) {
+    Geometry g;
+    if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
+    if (N < 0 || K < 0 || K % 256 != 0) return FQ_ERR_SHAPE;
+    if (N == 0) return FQ_OK;
+    if (!x || !w_packed || !y) return FQ_ERR_NULL;
+    if ((reinterpret_cast<uintptr_t>(w_packed) & 15) != 0) return FQ_ERR_ALIGN;
+    if (w2_packed && (reinterpret_cast<uintptr_t>(w2_packed) & 15) != 0) return FQ_ERR_ALIGN;
+    const bool dual = w2_packed != nullptr;
+    const int NV = dual ? 2 * N : N;  // rows the kernel walks
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    const DevInfo di = device_info(dev);
+    if (K == 0) {  // y = 0 (silu(0) * 0 = 0 for the fused form)
+        if (bias) return FQ_ERR_SHAPE;
+        e = fq::launch_zero(reinterpret_cast<uint32_t*>(y), (size_t)N, di.cus, st);
+        return e == hipSuccess ? FQ_OK : hip_fail(e);
+    }
+    int units = 0, records = 0;
+    fq::gemvp_geometry((int)dtype, K, &units, &records);
+    size_t lds = 0;
+    int wg = 0;
+    const void* fn =
+        fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, dual);
+    if (!fn || lds > std::min<size_t>(di.lds, 160 * 1024)) return FQ_ERR_SHAPE;
+    int per_cu = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wg, lds);
+    if (e != hipSuccess) return hip_fail(e);
+    if (per_cu < 1) return FQ_ERR_SHAPE;
+    const int wpb = wg / 64;
+    // one work-group per resident slot, each owning a contiguous row range
+    // with at least one row per wave, and whose row x K-slice partial sums fit
+    // its 4096-entry LDS buffer (slices of 64 lane units)
+    const long ns = (units + 63) / 64;
+    long G = (long)di.cus * per_cu;
+    G = std::max(1L, std::min<long>(G, ((long)NV + wpb - 1) / wpb));
+    auto max_rows = [&](long g) { return dual ? 2 * ((N + g - 1) / g) : (NV + g - 1) / g; };
+    G = std::max<long>(G, ((long)NV * ns + 4095) / 4096);
+    while (max_rows(G) * ns > 4096) ++G;
+    fq::GemvArgs a{};
+    a.x = x;
+    a.w = static_cast<const uint8_t*>(w_packed);
+    a.w2 = static_cast<const uint8_t*>(w2_packed);
+    a.y = y;
+    a.bias = bias;
+    a.bias_len = bias ? bias_len : 0;
+    a.bias_mode = bias ? 1 : 0;
+    a.M = 1;
+    a.K = K;
+    a.N = NV;
+    a.U = units;
+    a.Uc = records;
+    a.row_bytes = (int)fq::packed_row_bytes((int)dtype, K);
+    e = fq::launch_raw(fn, a, (int)G, wg, lds, st);
+    return e == hipSuccess ? FQ_OK : hip_fail(e);
+}
+
 }  // namespace
 
 extern "C" {
@@ -320,54 +383,39 @@ int fq_unpack_weights(uint32_t dtype, const void* w_packed, void* w_gguf, int N,
 
 int fq_gemv_packed(uint32_t dtype, const float* x, const void* w_packed, const float* bias,
                    int64_t bias_len, float* y, int K, int N, void* stream) {
+    return packed_gemv(dtype, x, w_packed, nullptr, bias, bias_len, y, K, N,
+                       static_cast<hipStream_t>(stream));
+}
+
+int fq_ffn_up_fused_packed(uint32_t dtype, const float* x, const void* w_gate_packed,
+                           const void* w_up_packed, float* y, int K, int N, void* stream) {
+    if (!w_up_packed) return FQ_ERR_NULL;
+    return packed_gemv(dtype, x, w_gate_packed, w_up_packed, nullptr, 0, y, K, N,
+                       static_cast<hipStream_t>(stream));
+}
+
+int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const void* w_up, float* y,
+                    int M, int K, int N, void* stream) {
     Geometry g;
     if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
-    if (N < 0 || K < 0 || K % 256 != 0) return FQ_ERR_SHAPE;
-    if (N == 0) return FQ_OK;
-    if (!x || !w_packed || !y) return FQ_ERR_NULL;
-    if ((reinterpret_cast<uintptr_t>(w_packed) & 15) != 0) return FQ_ERR_ALIGN;
+    if (M < 0 || N < 0 || K < 0 || K % g.be != 0) return FQ_ERR_SHAPE;
+    if (M == 0 || N == 0) return FQ_OK;
+    if (!x || !w_gate || !w_up || !y) return FQ_ERR_NULL;
     hipStream_t st = static_cast<hipStream_t>(stream);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e);
     const DevInfo di = device_info(dev);
-    if (K == 0) {
-        if (bias) return FQ_ERR_SHAPE;
-        e = fq::launch_zero(reinterpret_cast<uint32_t*>(y), (size_t)N, di.cus, st);
-        return e == hipSuccess ? FQ_OK : hip_fail(e);
-    }
-    int units = 0, records = 0;
-    fq::gemvp_geometry((int)dtype, K, &units, &records);
-    size_t lds = 0;
-    int wg = 0;
-    const void* fn = fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg);
-    if (!fn || lds > std::min<size_t>(di.lds, 160 * 1024)) return FQ_ERR_SHAPE;
-    int per_cu = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wg, lds);
+    uint8_t* buf = nullptr;
+    e = scratch(dev, st, 2 * (size_t)M * N * sizeof(float), &buf, 1);
     if (e != hipSuccess) return hip_fail(e);
-    if (per_cu < 1) return FQ_ERR_SHAPE;
-    const int wpb = wg / 64;
-    // one work-group per resident slot, each owning a contiguous row range
-    // with at least one row per wave, and whose row x K-slice partial sums fit
-    // its 4096-entry LDS buffer (slices of 64 lane units)
-    const long ns = (units + 63) / 64;
-    long G = (long)di.cus * per_cu;
-    G = std::max(1L, std::min<long>(G, ((long)N + wpb - 1) / wpb));
-    G = std::max<long>(G, ((long)N * ns + 4095) / 4096);
-    fq::GemvArgs a{};
-    a.x = x;
-    a.w = static_cast<const uint8_t*>(w_packed);
-    a.y = y;
-    a.bias = bias;
-    a.bias_len = bias ? bias_len : 0;
-    a.bias_mode = bias ? 1 : 0;
-    a.M = 1;
-    a.K = K;
-    a.N = N;
-    a.U = units;
-    a.Uc = records;
-    a.row_bytes = (int)fq::packed_row_bytes((int)dtype, K);
-    e = fq::launch_raw(fn, a, (int)G, wg, lds, st);
+    float* gate = reinterpret_cast<float*>(buf);
+    float* up = gate + (size_t)M * N;
+    int rc = run_matmul(dtype, x, w_gate, nullptr, 0, 0, gate, M, K, N, st);
+    if (rc != FQ_OK) return rc;
+    rc = run_matmul(dtype, x, w_up, nullptr, 0, 0, up, M, K, N, st);
+    if (rc != FQ_OK) return rc;
+    e = fq::launch_silu_mul(gate, up, y, (size_t)M * N, di.cus, st);
     return e == hipSuccess ? FQ_OK : hip_fail(e);
 }
 

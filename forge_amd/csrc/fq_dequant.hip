@@ -1,5 +1,6 @@
-// fq_dequant.hip -- the bit-exact dequant kernel (fq_dequant_rows) and a
-// small fill kernel used instead of memset nodes, so callers may capture it.
+// fq_dequant.hip -- the bit-exact dequant kernel (fq_dequant_rows) and small
+// elementwise kernels: a fill kernel used instead of memset nodes (so callers
+// may capture it) and the SiLU-multiply of the fused FFN.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -36,6 +37,25 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 __global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
         p[i] = 0u;
+}
+
+// y = silu(gate) * up = gate / (1 + exp(-gate)) * up, as the reference's
+// silu_multiply (src/operators/cpu/elementwise.cpp:89-150).
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gate,
+                                                       const float* __restrict__ up,
+                                                       float* __restrict__ y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const float g = gate[i];
+        y[i] = g / (1.0f + expf(-g)) * up[i];
+    }
+}
+
+hipError_t launch_silu_mul(const float* gate, const float* up, float* y, size_t n, int cus,
+                           hipStream_t st) {
+    const size_t want = (n + 255) / 256, cap = (size_t)cus * 8;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, st,
+                       gate, up, y, n);
+    return hipGetLastError();
 }
 
 hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st) {

@@ -225,10 +225,14 @@ __device__ __forceinline__ void next_step(It& t, int rows) {
     }
 }
 
-template <int F, int NL>
+// DUAL: two matrices of the same shape interleaved row by row (virtual row
+// 2n is row n of a.w, 2n + 1 row n of a.w2).
+template <int F, int NL, bool DUAL = false>
 __device__ __forceinline__ void pload(typename Pk<F>::Raw (&f)[NL], const GemvArgs& a,
                                       const It& t, int lo, int lane) {
-    const uint8_t* r = a.w + (size_t)min(lo + t.r, a.N - 1) * a.row_bytes;
+    const int v = min(lo + t.r, a.N - 1);
+    const uint8_t* r = DUAL ? ((v & 1) ? a.w2 : a.w) + (size_t)(v >> 1) * a.row_bytes
+                            : a.w + (size_t)v * a.row_bytes;
     const int v0 = t.s * 64 * NL;
 #pragma unroll
     for (int c = 0; c < NL; ++c) f[c] = Pk<F>::load(r, min(v0 + lane + 64 * c, a.U - 1), a.U);
@@ -255,7 +259,7 @@ __device__ __forceinline__ void advance_load(It& ld, It& q, const Claims& cl, in
 
 // One step of the compute side (slice cp.s of row lo + cp.r), then the loads
 // of the load side's step into the same registers.
-template <int F, int NL, int D, bool BIAS>
+template <int F, int NL, int D, bool BIAS, bool DUAL>
 __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& ld, It& q,
                                       const Claims& cl, const GemvArgs& a,
                                       Limbs (&L)[NL][Pk<F>::NREC], const uint8_t* lds,
@@ -273,7 +277,7 @@ __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& 
         const float t = Pk<F>::dot(f[c], min(v, a.U - 1), L[c]);
         acc += v < a.U ? t : 0.0f;
     }
-    pload<F, NL>(f, a, ld, lo, lane);
+    pload<F, NL, DUAL>(f, a, ld, lo, lane);
     float s = __builtin_bit_cast(
         float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
     if constexpr (BIAS) {
@@ -298,7 +302,9 @@ __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& 
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int F, int NL, int D, bool BIAS, int WG>
+// DUAL: y[n] = silu(x . w[n]) * (x . w2[n]) over a.N = 2 N virtual rows
+// (the fused FFN gate and up projections); work-group row ranges are even.
+template <int F, int NL, int D, bool BIAS, int WG, bool DUAL = false>
 __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     static_assert(D <= CR, "an item must span at least D steps");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -309,7 +315,9 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     const int ns = (a.U + 64 * NL - 1) / (64 * NL);
     const int G = gridDim.x, g = blockIdx.x;
     // the host sizes the grid so (hi - lo) * ns <= YBUF
-    const int lo = (int)((int64_t)a.N * g / G), hi = (int)((int64_t)a.N * (g + 1) / G);
+    const int lo = DUAL ? 2 * (int)((int64_t)(a.N / 2) * g / G) : (int)((int64_t)a.N * g / G);
+    const int hi = DUAL ? 2 * (int)((int64_t)(a.N / 2) * (g + 1) / G)
+                        : (int)((int64_t)a.N * (g + 1) / G);
     const int rows = hi - lo;
     const Claims cl{&ctr, rows * ns, rows};
 
@@ -327,7 +335,7 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     typename P::Raw f[D][NL];
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-        pload<F, NL>(f[j], a, ld, lo, lane);
+        pload<F, NL, DUAL>(f[j], a, ld, lo, lane);
         advance_load(ld, q, cl, lane);
     }
     Limbs L[NL][P::NREC];
@@ -340,13 +348,25 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     while (cp.n > 0) {
 #pragma unroll
         for (int j = 0; j < D; ++j)
-            pstep<F, NL, D, BIAS>(f[j], cp, ld, q, cl, a, L, lds, part, lo, lane, cur_s, res);
+            pstep<F, NL, D, BIAS, DUAL>(f[j], cp, ld, q, cl, a, L, lds, part, lo, lane, cur_s,
+                                        res);
     }
     __syncthreads();
-    for (int r = threadIdx.x; r < rows; r += WG) {
-        float v = part[r];
-        for (int s = 1; s < ns; ++s) v += part[s * rows + r];
-        a.y[lo + r] = v;
+    if constexpr (DUAL) {
+        for (int r = threadIdx.x; 2 * r < rows; r += WG) {
+            float gt = part[2 * r], up = part[2 * r + 1];
+            for (int s = 1; s < ns; ++s) {
+                gt += part[s * rows + 2 * r];
+                up += part[s * rows + 2 * r + 1];
+            }
+            a.y[(lo >> 1) + r] = gt / (1.0f + expf(-gt)) * up;  // silu(gate) * up
+        }
+    } else {
+        for (int r = threadIdx.x; r < rows; r += WG) {
+            float v = part[r];
+            for (int s = 1; s < ns; ++s) v += part[s * rows + r];
+            a.y[lo + r] = v;
+        }
     }
 }
 
@@ -364,6 +384,11 @@ const void* pfn(bool bias) {
     return pfn2<F, 1>(bias);
 }
 
+template <int F>
+const void* pfn_dual() {
+    return reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WGP, true>);
+}
+
 }  // namespace
 
 // Lane units per row and activation records for a packed GEMV of length K.
@@ -378,15 +403,17 @@ void gemvp_geometry(int dtype, int K, int* units, int* records) {
 }
 
 // Kernel for a row of `units` lane units: K-slices of 64 units (one per lane).
-const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg) {
+// dual: the fused gate/up form (bias unused).
+const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg,
+                            bool dual) {
     (void)units;
     const void* fn = nullptr;
     switch (dtype) {
-        case Q4_0: fn = pfn<Q4_0>(bias); break;
-        case Q4_1: fn = pfn<Q4_1>(bias); break;
-        case Q8_0: fn = pfn<Q8_0>(bias); break;
-        case Q4_K: fn = pfn<Q4_K>(bias); break;
-        case Q6_K: fn = pfn<Q6_K>(bias); break;
+        case Q4_0: fn = dual ? pfn_dual<Q4_0>() : pfn<Q4_0>(bias); break;
+        case Q4_1: fn = dual ? pfn_dual<Q4_1>() : pfn<Q4_1>(bias); break;
+        case Q8_0: fn = dual ? pfn_dual<Q8_0>() : pfn<Q8_0>(bias); break;
+        case Q4_K: fn = dual ? pfn_dual<Q4_K>() : pfn<Q4_K>(bias); break;
+        case Q6_K: fn = dual ? pfn_dual<Q6_K>() : pfn<Q6_K>(bias); break;
     }
     *lds = (size_t)records * RECB;
     *wg = WGP;

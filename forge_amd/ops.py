@@ -158,3 +158,36 @@ def gemv_packed(x: torch.Tensor, p: PackedWeight, bias: torch.Tensor | None = No
     _lib.check(_lib.lib().fq_gemv_packed(p.dtype, xv.data_ptr(), p.data.data_ptr(), bptr, blen,
                                          y.data_ptr(), p.K, p.N, _stream_ptr(x)), "fq_gemv_packed")
     return y
+
+
+def ffn_up_fused(x: torch.Tensor, w_gate: QWeight, w_up: QWeight) -> torch.Tensor:
+    """silu(x @ w_gate^T) * (x @ w_up^T) for GGUF weights, any M; mirrors
+    ops::ffn_up_fused (src/operators/cpu/matmul.cpp:1472-1533)."""
+    if x.dim() != 2:
+        raise RuntimeError("ffn_up_fused expects a 2D input")
+    M, K = x.shape
+    if (w_gate.dtype, w_gate.N, w_gate.K) != (w_up.dtype, w_up.N, w_up.K):
+        raise RuntimeError("ffn_up_fused: gate and up weights differ in dtype or shape")
+    if K != w_gate.K:
+        raise RuntimeError(f"ffn_up_fused dimension mismatch: K={K} K2={w_gate.K}")
+    x = x.contiguous()
+    y = torch.empty((M, w_gate.N), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_ffn_up_fused(w_gate.dtype, x.data_ptr(), w_gate.data.data_ptr(),
+                                          w_up.data.data_ptr(), y.data_ptr(), M, K, w_gate.N,
+                                          _stream_ptr(x)), "fq_ffn_up_fused")
+    return y
+
+
+def ffn_up_fused_packed(x: torch.Tensor, w_gate: PackedWeight, w_up: PackedWeight) -> torch.Tensor:
+    """Batch-1 fused gate/up over packed weights (x: [K] or [1, K]); returns [N]."""
+    xv = x.reshape(-1)
+    if (w_gate.dtype, w_gate.N, w_gate.K) != (w_up.dtype, w_up.N, w_up.K):
+        raise RuntimeError("ffn_up_fused: gate and up weights differ in dtype or shape")
+    if xv.numel() != w_gate.K:
+        raise RuntimeError(f"ffn_up_fused dimension mismatch: K={xv.numel()} K2={w_gate.K}")
+    y = torch.empty((w_gate.N,), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_ffn_up_fused_packed(w_gate.dtype, xv.data_ptr(),
+                                                 w_gate.data.data_ptr(), w_up.data.data_ptr(),
+                                                 y.data_ptr(), w_gate.K, w_gate.N,
+                                                 _stream_ptr(x)), "fq_ffn_up_fused_packed")
+    return y

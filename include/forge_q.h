@@ -133,6 +133,27 @@ int fq_unpack_weights(uint32_t dtype, const void* w_packed, void* w_gguf, int N,
 int fq_gemv_packed(uint32_t dtype, const float* x, const void* w_packed, const float* bias,
                    int64_t bias_len, float* y, int K, int N, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Fused FFN up-projection: y[m][n] = silu(x[m] . Wgate[n]) * (x[m] . Wup[n]),
+ * silu(g) = g / (1 + exp(-g)); Wgate and Wup have the same dtype and shape.
+ * ---------------------------------------------------------------------- */
+
+/* GGUF-layout weights, any M >= 1: two matmuls (as fq_matmul_transB) into a
+ * library-owned per-stream buffer, then the SiLU-multiply.  Replaces the
+ * device branch of ops::ffn_up_fused (matmul.cpp:1472-1533): the launchers
+ * cuda::launch_ffn_up_fused_q4_0 / _q4_k and their batch forms
+ * (cuda_fused.cu:15-106, 622-748) and the matmul_transB + silu_multiply
+ * fallback (elementwise.cpp:89-150). */
+int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const void* w_up, float* y,
+                    int M, int K, int N, void* stream);
+
+/* M = 1 over packed weights, one launch: the two matrices are walked as one
+ * GEMV of 2N interleaved rows, so the activation staging and the launch are
+ * shared, and the SiLU-multiply is applied when the row sums are written.
+ * Same results as fq_ffn_up_fused within the path's tolerance. */
+int fq_ffn_up_fused_packed(uint32_t dtype, const float* x, const void* w_gate_packed,
+                           const void* w_up_packed, float* y, int K, int N, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
