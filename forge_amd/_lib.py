@@ -40,6 +40,10 @@ SIGNATURES = {
     "fq_gemv_packed": (_I, [_U, _P, _P, _P, _L, _P, _I, _I, _P]),
     "fq_ffn_up_fused": (_I, [_U, _P, _P, _P, _P, _I, _I, _I, _P]),
     "fq_ffn_up_fused_packed": (_I, [_U, _P, _P, _P, _P, _I, _I, _P]),
+    "fq_fused_qkv": (_I, [_U, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "fq_fused_qkv_packed": (_I, [_U, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "fq_ffn_down_residual": (_I, [_U, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "fq_ffn_down_residual_packed": (_I, [_U, _P, _P, _P, _P, _I, _I, _P]),
 }
 
 _lib = None

@@ -207,18 +207,22 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     return run_mmq(dtype, g, x, w, bias, bias_mode, bias_len, y, M, K, N, dev, di, st);
 }
 
-// Batch-1 GEMV over packed rows; w2 != NULL: the fused gate/up form, y[n] =
-// silu(x . w[n]) * (x . w2[n]), run as one GEMV over 2 N interleaved rows.
+// Batch-1 GEMV over packed rows.  mode 0: y = x . w (+ bias).  mode 1 (fused
+// gate/up): y[n] = silu(x . w[n]) * (x . w2[n]), run as one GEMV over 2 N
+// interleaved rows.  mode 2 (fused QKV): y = [x . w | x . w2 | x . w3] with
+// n1 and n2 rows in w and w2 and N rows in all.
 int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
-                const float* bias, int64_t bias_len, float* y, int K, int N, hipStream_t st) {
+                const void* w3_packed, int n1, int n2, int mode, const float* bias,
+                int64_t bias_len, float* y, int K, int N, hipStream_t st) {
     Geometry g;
     if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
     if (N < 0 || K < 0 || K % 256 != 0) return FQ_ERR_SHAPE;
     if (N == 0) return FQ_OK;
     if (!x || !w_packed || !y) return FQ_ERR_NULL;
     if ((reinterpret_cast<uintptr_t>(w_packed) & 15) != 0) return FQ_ERR_ALIGN;
-    if (w2_packed && (reinterpret_cast<uintptr_t>(w2_packed) & 15) != 0) return FQ_ERR_ALIGN;
-    const bool dual = w2_packed != nullptr;
+    for (const void* p : {w2_packed, w3_packed})
+        if (p && (reinterpret_cast<uintptr_t>(p) & 15) != 0) return FQ_ERR_ALIGN;
+    const bool dual = mode == 1;
     const int NV = dual ? 2 * N : N;  // rows the kernel walks
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -234,7 +238,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     size_t lds = 0;
     int wg = 0;
     const void* fn =
-        fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, dual);
+        fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, mode);
     if (!fn || lds > std::min<size_t>(di.lds, 160 * 1024)) return FQ_ERR_SHAPE;
     int per_cu = 0;
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wg, lds);
@@ -254,6 +258,9 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     a.x = x;
     a.w = static_cast<const uint8_t*>(w_packed);
     a.w2 = static_cast<const uint8_t*>(w2_packed);
+    a.w3 = static_cast<const uint8_t*>(w3_packed);
+    a.n1 = n1;
+    a.n2 = n2;
     a.y = y;
     a.bias = bias;
     a.bias_len = bias ? bias_len : 0;
@@ -383,14 +390,81 @@ int fq_unpack_weights(uint32_t dtype, const void* w_packed, void* w_gguf, int N,
 
 int fq_gemv_packed(uint32_t dtype, const float* x, const void* w_packed, const float* bias,
                    int64_t bias_len, float* y, int K, int N, void* stream) {
-    return packed_gemv(dtype, x, w_packed, nullptr, bias, bias_len, y, K, N,
+    return packed_gemv(dtype, x, w_packed, nullptr, nullptr, 0, 0, 0, bias, bias_len, y, K, N,
                        static_cast<hipStream_t>(stream));
 }
 
 int fq_ffn_up_fused_packed(uint32_t dtype, const float* x, const void* w_gate_packed,
                            const void* w_up_packed, float* y, int K, int N, void* stream) {
     if (!w_up_packed) return FQ_ERR_NULL;
-    return packed_gemv(dtype, x, w_gate_packed, w_up_packed, nullptr, 0, y, K, N,
+    return packed_gemv(dtype, x, w_gate_packed, w_up_packed, nullptr, 0, 0, 1, nullptr, 0, y, K,
+                       N, static_cast<hipStream_t>(stream));
+}
+
+int fq_fused_qkv_packed(uint32_t dtype, const float* x, const void* wq, const void* wk,
+                        const void* wv, float* y, int K, int Nq, int Nk, int Nv, void* stream) {
+    if (Nq < 0 || Nk < 0 || Nv < 0 || (int64_t)Nq + Nk + Nv > INT32_MAX) return FQ_ERR_SHAPE;
+    if ((Nk && !wk) || (Nv && !wv)) return FQ_ERR_NULL;
+    return packed_gemv(dtype, x, wq, wk, wv, Nq, Nk, 2, nullptr, 0, y, K, Nq + Nk + Nv,
+                       static_cast<hipStream_t>(stream));
+}
+
+int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk, const void* wv,
+                 float* y, int M, int K, int Nq, int Nk, int Nv, void* stream) {
+    Geometry g;
+    if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
+    if (M < 0 || K < 0 || Nq < 0 || Nk < 0 || Nv < 0 || K % g.be != 0) return FQ_ERR_SHAPE;
+    if ((int64_t)Nq + Nk + Nv > INT32_MAX) return FQ_ERR_SHAPE;
+    const int Nt = Nq + Nk + Nv;
+    if (M == 0 || Nt == 0) return FQ_OK;
+    if (!x || !y || (Nq && !wq) || (Nk && !wk) || (Nv && !wv)) return FQ_ERR_NULL;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const void* ws[3] = {wq, wk, wv};
+    const int ns[3] = {Nq, Nk, Nv};
+    if (M == 1) {  // the three outputs are contiguous slices of y
+        int off = 0;
+        for (int i = 0; i < 3; ++i) {
+            if (ns[i] > 0) {
+                const int rc = run_matmul(dtype, x, ws[i], nullptr, 0, 0, y + off, 1, K, ns[i], st);
+                if (rc != FQ_OK) return rc;
+            }
+            off += ns[i];
+        }
+        return FQ_OK;
+    }
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    const DevInfo di = device_info(dev);
+    uint8_t* buf = nullptr;
+    const int nmax = std::max(Nq, std::max(Nk, Nv));
+    e = scratch(dev, st, (size_t)M * nmax * sizeof(float), &buf, 1);
+    if (e != hipSuccess) return hip_fail(e);
+    float* tmp = reinterpret_cast<float*>(buf);
+    int off = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (ns[i] > 0) {
+            const int rc = run_matmul(dtype, x, ws[i], nullptr, 0, 0, tmp, M, K, ns[i], st);
+            if (rc != FQ_OK) return rc;
+            e = fq::launch_copy_cols(tmp, y, M, ns[i], Nt, off, di.cus, st);
+            if (e != hipSuccess) return hip_fail(e);
+        }
+        off += ns[i];
+    }
+    return FQ_OK;
+}
+
+int fq_ffn_down_residual(uint32_t dtype, const float* x, const void* w, const float* residual,
+                         float* y, int M, int K, int N, void* stream) {
+    if (!residual) return FQ_ERR_NULL;
+    return run_matmul(dtype, x, w, residual, 2, (int64_t)M * N, y, M, K, N,
+                      static_cast<hipStream_t>(stream));
+}
+
+int fq_ffn_down_residual_packed(uint32_t dtype, const float* x, const void* w_packed,
+                                const float* residual, float* y, int K, int N, void* stream) {
+    if (!residual) return FQ_ERR_NULL;
+    return packed_gemv(dtype, x, w_packed, nullptr, nullptr, 0, 0, 0, residual, N, y, K, N,
                        static_cast<hipStream_t>(stream));
 }
 

@@ -58,6 +58,27 @@ hipError_t launch_silu_mul(const float* gate, const float* up, float* y, size_t 
     return hipGetLastError();
 }
 
+// y[m][off + n] = src[m][n]: places one matrix's outputs into the
+// concatenated rows of a fused QKV result.
+__global__ __launch_bounds__(256) void copy_cols_kernel(const float* __restrict__ src,
+                                                        float* __restrict__ y, int M, int n_src,
+                                                        int ld, int off) {
+    const size_t total = (size_t)M * n_src;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * 256) {
+        const int m = (int)(i / n_src), n = (int)(i % n_src);
+        y[(size_t)m * ld + off + n] = src[i];
+    }
+}
+
+hipError_t launch_copy_cols(const float* src, float* y, int M, int n_src, int ld, int off, int cus,
+                            hipStream_t st) {
+    const size_t want = ((size_t)M * n_src + 255) / 256, cap = (size_t)cus * 8;
+    hipLaunchKernelGGL(copy_cols_kernel, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0,
+                       st, src, y, M, n_src, ld, off);
+    return hipGetLastError();
+}
+
 hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st) {
     hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(256), 0, st, p, n);
     return hipGetLastError();

@@ -225,14 +225,26 @@ __device__ __forceinline__ void next_step(It& t, int rows) {
     }
 }
 
-// DUAL: two matrices of the same shape interleaved row by row (virtual row
-// 2n is row n of a.w, 2n + 1 row n of a.w2).
-template <int F, int NL, bool DUAL = false>
+// Row sources.  ONE: row v of a.w.  PAIR: two matrices of the same shape
+// interleaved row by row (virtual row 2n is row n of a.w, 2n + 1 row n of
+// a.w2).  CAT: a.w, a.w2, a.w3 stacked (a.n1 and a.n2 rows in the first two).
+enum { ONE = 0, PAIR = 1, CAT = 2 };
+
+template <int MODE>
+__device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int v) {
+    if constexpr (MODE == PAIR) return ((v & 1) ? a.w2 : a.w) + (size_t)(v >> 1) * a.row_bytes;
+    if constexpr (MODE == CAT) {
+        const int n12 = a.n1 + a.n2;
+        const uint8_t* base = v < a.n1 ? a.w : v < n12 ? a.w2 : a.w3;
+        return base + (size_t)(v - (v < a.n1 ? 0 : v < n12 ? a.n1 : n12)) * a.row_bytes;
+    }
+    return a.w + (size_t)v * a.row_bytes;
+}
+
+template <int F, int NL, int MODE = ONE>
 __device__ __forceinline__ void pload(typename Pk<F>::Raw (&f)[NL], const GemvArgs& a,
                                       const It& t, int lo, int lane) {
-    const int v = min(lo + t.r, a.N - 1);
-    const uint8_t* r = DUAL ? ((v & 1) ? a.w2 : a.w) + (size_t)(v >> 1) * a.row_bytes
-                            : a.w + (size_t)v * a.row_bytes;
+    const uint8_t* r = row_ptr<MODE>(a, min(lo + t.r, a.N - 1));
     const int v0 = t.s * 64 * NL;
 #pragma unroll
     for (int c = 0; c < NL; ++c) f[c] = Pk<F>::load(r, min(v0 + lane + 64 * c, a.U - 1), a.U);
@@ -259,7 +271,7 @@ __device__ __forceinline__ void advance_load(It& ld, It& q, const Claims& cl, in
 
 // One step of the compute side (slice cp.s of row lo + cp.r), then the loads
 // of the load side's step into the same registers.
-template <int F, int NL, int D, bool BIAS, bool DUAL>
+template <int F, int NL, int D, bool BIAS, int MODE>
 __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& ld, It& q,
                                       const Claims& cl, const GemvArgs& a,
                                       Limbs (&L)[NL][Pk<F>::NREC], const uint8_t* lds,
@@ -277,7 +289,7 @@ __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& 
         const float t = Pk<F>::dot(f[c], min(v, a.U - 1), L[c]);
         acc += v < a.U ? t : 0.0f;
     }
-    pload<F, NL, DUAL>(f, a, ld, lo, lane);
+    pload<F, NL, MODE>(f, a, ld, lo, lane);
     float s = __builtin_bit_cast(
         float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
     if constexpr (BIAS) {
@@ -302,10 +314,12 @@ __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& 
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// DUAL: y[n] = silu(x . w[n]) * (x . w2[n]) over a.N = 2 N virtual rows
-// (the fused FFN gate and up projections); work-group row ranges are even.
-template <int F, int NL, int D, bool BIAS, int WG, bool DUAL = false>
+// MODE PAIR: y[n] = silu(x . w[n]) * (x . w2[n]) over a.N = 2 N virtual
+// rows (the fused FFN gate and up projections); work-group row ranges are
+// even.  MODE CAT: y is the concatenation of the three GEMVs (fused QKV).
+template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE>
 __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
+    constexpr bool DUAL = MODE == PAIR;
     static_assert(D <= CR, "an item must span at least D steps");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int ctr;
@@ -335,7 +349,7 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     typename P::Raw f[D][NL];
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-        pload<F, NL, DUAL>(f[j], a, ld, lo, lane);
+        pload<F, NL, MODE>(f[j], a, ld, lo, lane);
         advance_load(ld, q, cl, lane);
     }
     Limbs L[NL][P::NREC];
@@ -348,7 +362,7 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     while (cp.n > 0) {
 #pragma unroll
         for (int j = 0; j < D; ++j)
-            pstep<F, NL, D, BIAS, DUAL>(f[j], cp, ld, q, cl, a, L, lds, part, lo, lane, cur_s,
+            pstep<F, NL, D, BIAS, MODE>(f[j], cp, ld, q, cl, a, L, lds, part, lo, lane, cur_s,
                                         res);
     }
     __syncthreads();
@@ -385,8 +399,9 @@ const void* pfn(bool bias) {
 }
 
 template <int F>
-const void* pfn_dual() {
-    return reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WGP, true>);
+const void* pfn_mode(int mode) {
+    return mode == PAIR ? reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WGP, PAIR>)
+                        : reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WGP, CAT>);
 }
 
 }  // namespace
@@ -403,17 +418,17 @@ void gemvp_geometry(int dtype, int K, int* units, int* records) {
 }
 
 // Kernel for a row of `units` lane units: K-slices of 64 units (one per lane).
-// dual: the fused gate/up form (bias unused).
+// mode 1: the fused gate/up form, 2: the fused QKV form (bias unused in both).
 const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg,
-                            bool dual) {
+                            int mode) {
     (void)units;
     const void* fn = nullptr;
     switch (dtype) {
-        case Q4_0: fn = dual ? pfn_dual<Q4_0>() : pfn<Q4_0>(bias); break;
-        case Q4_1: fn = dual ? pfn_dual<Q4_1>() : pfn<Q4_1>(bias); break;
-        case Q8_0: fn = dual ? pfn_dual<Q8_0>() : pfn<Q8_0>(bias); break;
-        case Q4_K: fn = dual ? pfn_dual<Q4_K>() : pfn<Q4_K>(bias); break;
-        case Q6_K: fn = dual ? pfn_dual<Q6_K>() : pfn<Q6_K>(bias); break;
+        case Q4_0: fn = mode ? pfn_mode<Q4_0>(mode) : pfn<Q4_0>(bias); break;
+        case Q4_1: fn = mode ? pfn_mode<Q4_1>(mode) : pfn<Q4_1>(bias); break;
+        case Q8_0: fn = mode ? pfn_mode<Q8_0>(mode) : pfn<Q8_0>(bias); break;
+        case Q4_K: fn = mode ? pfn_mode<Q4_K>(mode) : pfn<Q4_K>(bias); break;
+        case Q6_K: fn = mode ? pfn_mode<Q6_K>(mode) : pfn<Q6_K>(bias); break;
     }
     *lds = (size_t)records * RECB;
     *wg = WGP;

@@ -10,7 +10,9 @@ namespace fq {
 struct GemvArgs {
     const float* x;       // [M][K]
     const uint8_t* w;     // [N] rows of row_bytes
-    const uint8_t* w2;    // fused gate/up: the up matrix (w is the gate matrix)
+    const uint8_t* w2;    // fused gate/up: the up matrix (w is the gate matrix); QKV: K
+    const uint8_t* w3;    // fused QKV: V (w is Q, w2 is K)
+    int n1, n2;           // fused QKV: rows of Q and K
     float* y;             // [M][N]
     const float* bias;    // optional, see bias_mode
     int64_t bias_len;
@@ -32,12 +34,15 @@ hipError_t launch_raw(const void* fn, const GemvArgs& a, int grid, int wg, size_
 // packed-layout batch-1 kernels (fq_gemvp.hip)
 void gemvp_geometry(int dtype, int K, int* units, int* records);
 const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg,
-                            bool dual = false);
+                            int mode = 0);
 hipError_t launch_pack(int dtype, const uint8_t* src, uint8_t* dst, int N, int K, bool pack,
                        int grid, hipStream_t st);
 hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st);
 hipError_t launch_silu_mul(const float* gate, const float* up, float* y, size_t n, int cus,
                            hipStream_t st);
+// y[m][off + n] = src[m][n] for n < n_src (rows of y are ld floats long)
+hipError_t launch_copy_cols(const float* src, float* y, int M, int n_src, int ld, int off, int cus,
+                            hipStream_t st);
 // M > 1 on MFMA (fq_mmq.hip)
 struct MmqArgs {
     const uint8_t* w;     // GGUF rows

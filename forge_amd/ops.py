@@ -191,3 +191,73 @@ def ffn_up_fused_packed(x: torch.Tensor, w_gate: PackedWeight, w_up: PackedWeigh
                                                  y.data_ptr(), w_gate.K, w_gate.N,
                                                  _stream_ptr(x)), "fq_ffn_up_fused_packed")
     return y
+
+
+def _same_k(name, K, *ws):
+    for w in ws:
+        if w.K != K:
+            raise RuntimeError(f"{name} dimension mismatch: K={K} K2={w.K}")
+    if len({w.dtype for w in ws}) != 1:
+        raise RuntimeError(f"{name}: weights differ in dtype")
+
+
+def fused_qkv(x: torch.Tensor, wq: QWeight, wk: QWeight, wv: QWeight) -> torch.Tensor:
+    """[x Wq^T | x Wk^T | x Wv^T] for GGUF weights, any M; mirrors
+    matmul_transB_fused_qkv_q4_0 / _q4_k (src/operators/cpu/matmul.cpp:1535-1600)."""
+    if x.dim() != 2:
+        raise RuntimeError("fused_qkv expects a 2D input")
+    M, K = x.shape
+    _same_k("fused_qkv", K, wq, wk, wv)
+    x = x.contiguous()
+    y = torch.empty((M, wq.N + wk.N + wv.N), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_fused_qkv(wq.dtype, x.data_ptr(), wq.data.data_ptr(),
+                                       wk.data.data_ptr(), wv.data.data_ptr(), y.data_ptr(), M, K,
+                                       wq.N, wk.N, wv.N, _stream_ptr(x)), "fq_fused_qkv")
+    return y
+
+
+def fused_qkv_packed(x: torch.Tensor, wq: PackedWeight, wk: PackedWeight,
+                     wv: PackedWeight) -> torch.Tensor:
+    """Batch-1 fused QKV over packed weights (x: [K] or [1, K]); returns [Nq + Nk + Nv]."""
+    xv = x.reshape(-1)
+    _same_k("fused_qkv", xv.numel(), wq, wk, wv)
+    y = torch.empty((wq.N + wk.N + wv.N,), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_fused_qkv_packed(wq.dtype, xv.data_ptr(), wq.data.data_ptr(),
+                                              wk.data.data_ptr(), wv.data.data_ptr(),
+                                              y.data_ptr(), wq.K, wq.N, wk.N, wv.N,
+                                              _stream_ptr(x)), "fq_fused_qkv_packed")
+    return y
+
+
+def ffn_down_residual(x: torch.Tensor, w: QWeight, residual: torch.Tensor) -> torch.Tensor:
+    """x W^T + residual for GGUF weights, any M; mirrors
+    matmul_transB_fused_ffn_down_residual_q4_0 / _q6_k (matmul.cpp:1601-1637)."""
+    if x.dim() != 2 or residual.dim() != 2:
+        raise RuntimeError("ffn_down_residual expects 2D tensors")
+    M, K = x.shape
+    _same_k("ffn_down_residual", K, w)
+    if tuple(residual.shape) != (M, w.N):
+        raise RuntimeError("ffn_down_residual: residual shape mismatch")
+    x = x.contiguous()
+    r = residual.to(device=x.device, dtype=torch.float32).contiguous()
+    y = torch.empty((M, w.N), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_ffn_down_residual(w.dtype, x.data_ptr(), w.data.data_ptr(),
+                                               r.data_ptr(), y.data_ptr(), M, K, w.N,
+                                               _stream_ptr(x)), "fq_ffn_down_residual")
+    return y
+
+
+def ffn_down_residual_packed(x: torch.Tensor, w: PackedWeight,
+                             residual: torch.Tensor) -> torch.Tensor:
+    """Batch-1 x W^T + residual over packed weights; returns [N]."""
+    xv = x.reshape(-1)
+    _same_k("ffn_down_residual", xv.numel(), w)
+    r = residual.reshape(-1).to(device=x.device, dtype=torch.float32).contiguous()
+    if r.numel() != w.N:
+        raise RuntimeError("ffn_down_residual: residual shape mismatch")
+    y = torch.empty((w.N,), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().fq_ffn_down_residual_packed(w.dtype, xv.data_ptr(), w.data.data_ptr(),
+                                                      r.data_ptr(), y.data_ptr(), w.K, w.N,
+                                                      _stream_ptr(x)),
+               "fq_ffn_down_residual_packed")
+    return y

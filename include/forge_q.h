@@ -154,6 +154,37 @@ int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const vo
 int fq_ffn_up_fused_packed(uint32_t dtype, const float* x, const void* w_gate_packed,
                            const void* w_up_packed, float* y, int K, int N, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Fused QKV projection: y[m] = [x[m] . Wq^T | x[m] . Wk^T | x[m] . Wv^T],
+ * rows of y are Nq + Nk + Nv floats.  The three weights share dtype and K.
+ * ---------------------------------------------------------------------- */
+
+/* GGUF-layout weights, any M >= 1.  Replaces matmul_transB_fused_qkv_q4_0 /
+ * _q4_k (matmul.cpp:1535-1600, 1639-1692) and the CUDA fused QKV launcher
+ * (cuda_fused.cu:924-1024); at M > 1 the three results pass through a
+ * library-owned per-stream buffer. */
+int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk, const void* wv,
+                 float* y, int M, int K, int Nq, int Nk, int Nv, void* stream);
+
+/* M = 1 over packed weights in one launch (the activation staging is shared). */
+int fq_fused_qkv_packed(uint32_t dtype, const float* x, const void* wq_packed,
+                        const void* wk_packed, const void* wv_packed, float* y, int K, int Nq,
+                        int Nk, int Nv, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused FFN down-projection + residual: y = x . W^T + residual, residual
+ * [M][N] on the device.  Replaces matmul_transB_fused_ffn_down_residual_q4_0
+ * / _q6_k (matmul.cpp:1601-1637, 1729-1764) and the CUDA launcher
+ * (cuda_fused.cu:750-837): the residual is added when the row sums are
+ * written, so there is no separate add pass.
+ * ---------------------------------------------------------------------- */
+int fq_ffn_down_residual(uint32_t dtype, const float* x, const void* w, const float* residual,
+                         float* y, int M, int K, int N, void* stream);
+
+/* M = 1 over packed weights. */
+int fq_ffn_down_residual_packed(uint32_t dtype, const float* x, const void* w_packed,
+                                const float* residual, float* y, int K, int N, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

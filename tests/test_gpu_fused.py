@@ -1,4 +1,5 @@
-"""GPU parity of the fused FFN up-projection, silu(x Wg^T) * (x Wu^T).
+"""GPU parity of the fused decode ops: FFN up-projection silu(x Wg^T) * (x Wu^T),
+QKV projection [x Wq^T | x Wk^T | x Wv^T] and down-projection + residual.
 
 Mirrors ops::ffn_up_fused (reference matmul.cpp:1472-1533).  The oracle is
 the exact product: the fp64 matmuls over the bit-exact dequantized weights,
@@ -88,3 +89,59 @@ def test_fused_errors():
     # K = 0 and an empty batch are no-ops / zeros, as in the matmul entry points
     y = ops.ffn_up_fused(torch.zeros((0, K), device="cuda"), Wg, dev_weight(F.Q4_0, wu, N, K))
     assert y.shape == (0, N)
+
+
+def assert_matmul(y, ref, x, w_blocks_list, dtype, K, what):
+    from helpers import assert_close
+    deq = np.concatenate([oracle.dequant(dtype, wb, wb.shape[0], K) for wb in w_blocks_list])
+    assert_close(y, ref, x, np.array([float(np.max(np.abs(deq)))]), what)
+
+
+@pytest.mark.parametrize("dtype", ALL)
+@pytest.mark.parametrize("M", [1, 4, 37])
+def test_fused_qkv_gguf(dtype, M):
+    K, Nq, Nk, Nv = 1024, 512, 128, 96
+    ws = [synth.make_weights(dtype, n, K, 30 + i) for i, n in enumerate((Nq, Nk, Nv))]
+    x = synth.make_x(M, K, seed=M + 1)
+    y = ops.fused_qkv(torch.from_numpy(x).cuda(), *(dev_weight(dtype, w, n, K)
+                                                    for w, n in zip(ws, (Nq, Nk, Nv))))
+    ref = np.concatenate([oracle.matmul_f64(dtype, x, w, n, K) for w, n in zip(ws, (Nq, Nk, Nv))],
+                         axis=1)
+    assert_matmul(y.cpu().numpy(), ref, x, ws, dtype, K, f"{F.fmt(dtype).name} qkv M={M}")
+
+
+@pytest.mark.parametrize("name,dtype,K,Nq,Nk,Nv", [
+    ("tinyllama-q4_0", F.Q4_0, 2048, 2048, 256, 256),
+    ("qwen7b-q4_k", F.Q4_K, 3584, 3584, 512, 512),
+    ("q6_k-odd", F.Q6_K, 1024, 77, 0, 33),
+    ("q8_0", F.Q8_0, 2048, 300, 50, 50),
+])
+def test_fused_qkv_packed(name, dtype, K, Nq, Nk, Nv):
+    ns = (Nq, Nk, Nv)
+    ws = [synth.make_weights(dtype, max(n, 1), K, 40 + i) for i, n in enumerate(ns)]
+    Ps = [ops.pack_weights(dev_weight(dtype, w, max(n, 1), K)) for w, n in zip(ws, ns)]
+    for P, n in zip(Ps, ns):
+        P.N = n  # a zero-row matrix keeps a valid buffer
+    x = synth.make_x(1, K, seed=5)
+    y = ops.fused_qkv_packed(torch.from_numpy(x).cuda(), *Ps)
+    ref = np.concatenate([oracle.matmul_f64(dtype, x, w, n, K) if n else np.zeros((1, 0))
+                          for w, n in zip(ws, ns)], axis=1)
+    assert_matmul(y.cpu().numpy().reshape(1, -1), ref, x, [w for w, n in zip(ws, ns) if n],
+                  dtype, K, name)
+
+
+@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q6_K, F.Q4_K])
+@pytest.mark.parametrize("M", [1, 3, 50])
+def test_ffn_down_residual(dtype, M):
+    K, N = 2048, 300
+    w = synth.make_weights(dtype, N, K, 51)
+    x = synth.make_x(M, K, seed=52)
+    r = synth.make_x(M, N, seed=53)
+    W = dev_weight(dtype, w, N, K)
+    y = ops.ffn_down_residual(torch.from_numpy(x).cuda(), W, torch.from_numpy(r).cuda())
+    ref = oracle.matmul_f64(dtype, x, w, N, K) + r
+    assert_matmul(y.cpu().numpy(), ref, x, [w], dtype, K, f"{F.fmt(dtype).name} down+res M={M}")
+    if M == 1:
+        yp = ops.ffn_down_residual_packed(torch.from_numpy(x).cuda(), ops.pack_weights(W),
+                                          torch.from_numpy(r).cuda())
+        assert_matmul(yp.cpu().numpy().reshape(1, -1), ref, x, [w], dtype, K, "packed")
