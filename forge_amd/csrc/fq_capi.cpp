@@ -42,9 +42,17 @@ bool geometry(uint32_t dtype, Geometry& g) {
         case FQ_DTYPE_Q8_0: g = {32, 34, 1}; return true;
         case FQ_DTYPE_Q4_K: g = {256, 144, 2}; return true;
         case FQ_DTYPE_Q6_K: g = {256, 210, 4}; return true;
+        case FQ_DTYPE_Q5_0: g = {32, 22, 1}; return true;
+        case FQ_DTYPE_Q5_1: g = {32, 24, 1}; return true;
+        case FQ_DTYPE_Q3_K: g = {256, 110, 4}; return true;
+        case FQ_DTYPE_Q5_K: g = {256, 176, 2}; return true;
+        case FQ_DTYPE_IQ4_NL: g = {32, 18, 1}; return true;
         default: return false;
     }
 }
+
+// Formats with the aligned packed layout (fq_pack.h).
+bool packable(uint32_t dtype) { return fq::packed_row_bytes((int)dtype, 256) > 0; }
 
 struct DevInfo {
     int cus = 0;
@@ -215,7 +223,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
                 const void* w3_packed, int n1, int n2, int mode, const float* bias,
                 int64_t bias_len, float* y, int K, int N, hipStream_t st) {
     Geometry g;
-    if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
+    if (!geometry(dtype, g) || !packable(dtype)) return FQ_ERR_DTYPE;
     if (N < 0 || K < 0 || K % 256 != 0) return FQ_ERR_SHAPE;
     if (N == 0) return FQ_OK;
     if (!x || !w_packed || !y) return FQ_ERR_NULL;
@@ -353,14 +361,14 @@ int fq_dequant_rows(uint32_t dtype, const void* w, float* out, int N, int K, voi
 
 int64_t fq_packed_row_bytes(uint32_t dtype, int K) {
     Geometry g;
-    if (!geometry(dtype, g) || K <= 0 || K % 256 != 0) return 0;
+    if (!geometry(dtype, g) || !packable(dtype) || K <= 0 || K % 256 != 0) return 0;
     return fq::packed_row_bytes((int)dtype, K);
 }
 
 static int pack_common(uint32_t dtype, const void* src, void* dst, int N, int K, bool pack,
                        void* stream) {
     Geometry g;
-    if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
+    if (!geometry(dtype, g) || !packable(dtype)) return FQ_ERR_DTYPE;
     if (N < 0 || K < 0 || K % 256 != 0) return FQ_ERR_SHAPE;
     if (N == 0 || K == 0) return FQ_OK;
     if (!src || !dst) return FQ_ERR_NULL;

@@ -86,19 +86,11 @@ hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st) {
 
 hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,
                           int row_bytes, int grid, hipStream_t st) {
-#define FQ_DQ(F)                                                                              \
-    hipLaunchKernelGGL(dequant_kernel<F>, dim3(grid), dim3(256), 0, st, w, out, N, K, U,      \
-                       row_bytes);                                                            \
-    return hipGetLastError();
-    switch (dtype) {
-        case Q4_0: FQ_DQ(Q4_0)
-        case Q4_1: FQ_DQ(Q4_1)
-        case Q8_0: FQ_DQ(Q8_0)
-        case Q4_K: FQ_DQ(Q4_K)
-        case Q6_K: FQ_DQ(Q6_K)
-        default: return hipErrorInvalidValue;
-    }
-#undef FQ_DQ
+return with_format(dtype, hipErrorInvalidValue, [&](auto f) {
+        hipLaunchKernelGGL(dequant_kernel<decltype(f)::value>, dim3(grid), dim3(256), 0, st, w,
+                           out, N, K, U, row_bytes);
+        return hipGetLastError();
+    });
 }
 
 }  // namespace fq

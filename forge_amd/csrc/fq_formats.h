@@ -1,4 +1,4 @@
-// fq_formats.h -- device-side decoding of the five GGUF block formats.
+// fq_formats.h -- device-side decoding of the ten GGUF block formats.
 //
 // Every format is processed in "units" of 32 weights.  A unit is what one
 // lane decodes per step: a whole block for Q4_0/Q4_1/Q8_0, one eighth of a
@@ -17,6 +17,12 @@
 //   Q8_0  (d, -128 d)          matmul.cpp:106-118   w = (q' - 128) d, q' = q ^ 0x80
 //   Q4_K  (d sc_g, -dmin m_g)  matmul.cpp:340-377   w = d sc q - dmin m
 //   Q6_K  (d sc_g, -32 d sc_g) matmul.cpp:242-279   w = (d sc)(q - 32)
+//   Q5_0  (d, -16 d)           matmul.cpp:125-152   w = (q - 16) d
+//   Q5_1  (d, m)               matmul.cpp:156-186   w = q d + m
+//   Q3_K  (d sc_g, -4 d sc_g)  matmul.cpp:284-338   w = (d sc)(q - 4)
+//   Q5_K  (d sc_g, -dmin m_g)  matmul.cpp:382-415   w = d sc q - dmin m
+//   IQ4_NL (d, 0)              matmul.cpp:849-868   w = d T[q]; the "code" of
+//         a slot is the table value T[q] itself (signed), not the index
 // S_g is computed once per staged activation vector, so the offsets cost one
 // FMA per group instead of one operation per weight.
 #pragma once
@@ -26,7 +32,33 @@
 
 namespace fq {
 
-enum : int { Q4_0 = 2, Q4_1 = 3, Q4_K = 4, Q8_0 = 7, Q6_K = 13 };
+enum : int {
+    Q4_0 = 2, Q4_1 = 3, Q4_K = 4, Q8_0 = 7, Q5_0 = 8, Q5_1 = 9, Q3_K = 11, Q5_K = 12,
+    Q6_K = 13, IQ4_NL = 17
+};
+
+// Calls fn(FmtTag<F>{}) for the format F named by dtype (the forge::DataType
+// value); returns dflt for any other dtype.
+template <int F>
+struct FmtTag {
+    static constexpr int value = F;
+};
+template <class R, class Fn>
+__host__ __device__ inline R with_format(int dtype, R dflt, Fn&& fn) {
+    switch (dtype) {
+        case Q4_0: return fn(FmtTag<Q4_0>{});
+        case Q4_1: return fn(FmtTag<Q4_1>{});
+        case Q4_K: return fn(FmtTag<Q4_K>{});
+        case Q8_0: return fn(FmtTag<Q8_0>{});
+        case Q5_0: return fn(FmtTag<Q5_0>{});
+        case Q5_1: return fn(FmtTag<Q5_1>{});
+        case Q3_K: return fn(FmtTag<Q3_K>{});
+        case Q5_K: return fn(FmtTag<Q5_K>{});
+        case Q6_K: return fn(FmtTag<Q6_K>{});
+        case IQ4_NL: return fn(FmtTag<IQ4_NL>{});
+        default: return dflt;
+    }
+}
 
 // ---- loads: GGUF blocks are only 2-byte aligned; gfx950 global loads accept
 // unaligned addresses, and hipcc lowers these to single dwordx{1,2,4} loads.
@@ -330,6 +362,256 @@ struct Fmt<Q6_K> {
     __device__ static float value(float q, float A, float) { return A * (q - 32.0f); }
 };
 
+
+// ------------------------------------------------- bit helpers (5-bit, IQ4_NL)
+// Bits 0..3 of v spread to bit 0 of bytes 0..3.  The multiplier places bit b
+// at 8 b (and at b + 7 j for j != b, which the mask drops); the partial
+// products never overlap, so there are no carries.
+__device__ __forceinline__ uint32_t spread4(uint32_t v) {
+    return __umul24(v & 15u, 0x00204081u) & 0x01010101u;
+}
+// 5-bit codes of four slots: the nibbles n (in bits 0..3 of each byte) with
+// bits 0..3 of hb as bit 4.
+__device__ __forceinline__ uint32_t five_bit(uint32_t n, uint32_t hb) {
+    return n | (spread4(hb) << 4);
+}
+
+// IQ4_NL table (matmul.cpp:849-851) as int8 bytes, four per dword.
+constexpr uint32_t IQ4T0 = 0xBFAD9881u, IQ4T1 = 0xF6EADDCFu, IQ4T2 = 0x26190D01u,
+                   IQ4T3 = 0x71594535u;
+// Four 4-bit indices (bits 0..3 of each byte of idx) -> four int8 table values.
+// v_perm_b32 picks bytes 0..7 of a dword pair: entries 0..7 and 8..15 come
+// from two lookups on idx & 7, and bit 3 of each index selects between them.
+__device__ __forceinline__ uint32_t iq4_lookup(uint32_t idx) {
+    const uint32_t lo7 = idx & 0x07070707u;
+    const uint32_t a = __builtin_amdgcn_perm(IQ4T1, IQ4T0, lo7);
+    const uint32_t b = __builtin_amdgcn_perm(IQ4T3, IQ4T2, lo7);
+    const uint32_t sel = ((idx >> 3) & 0x01010101u) * 0xFFu;
+    return (b & sel) | (a & ~sel);
+}
+
+// ---------------------------------------------------------------- Q5_0 (22 B)
+// Block: d f16 @0, qh u32 @2, qs[16] @6.  Element j: nibble j % 16 of qs
+// (low for j < 16) plus 16 times bit j of qh.  Slots are elements.
+template <>
+struct Fmt<Q5_0> {
+    static constexpr int BE = 32, BB = 22, NG = 1;
+    struct Raw {
+        uint32_t d, qh;
+        uint4 qs;
+    };
+    __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    template <bool NT = false>
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 22 * u;
+        return Raw{ldg16<NT>(p), ldg32<NT>(p + 2), ldg128<NT>(p + 6)};
+    }
+    // 5-bit codes of slots 4i..4i+3 (lo) and 16+4i.. (hi)
+    __device__ static void codes(uint32_t w, uint32_t qh, int i, uint32_t& lo, uint32_t& hi) {
+        lo = five_bit(w & 0x0F0F0F0Fu, qh >> (4 * i));
+        hi = five_bit((w >> 4) & 0x0F0F0F0Fu, qh >> (16 + 4 * i));
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
+        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo, hi;
+            codes(w[i], r.qh, i, lo, hi);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                q[4 * i + b] = ubyte(lo, b);
+                q[16 + 4 * i + b] = ubyte(hi, b);
+            }
+        }
+        const float d = f16<EXACT>(r.d);
+        A[0] = d;
+        B[0] = -16.0f * d;
+    }
+    __device__ static float value(float q, float A, float) { return (q - 16.0f) * A; }
+};
+
+// ---------------------------------------------------------------- Q5_1 (24 B)
+// Block: d f16 @0, m f16 @2, qh u32 @4, qs[16] @8; codes as Q5_0.
+template <>
+struct Fmt<Q5_1> {
+    static constexpr int BE = 32, BB = 24, NG = 1;
+    struct Raw {
+        uint32_t dm, qh;
+        uint4 qs;
+    };
+    __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    template <bool NT = false>
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 24 * u;
+        return Raw{ldg32<NT>(p), ldg32<NT>(p + 4), ldg128<NT>(p + 8)};
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
+        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo, hi;
+            Fmt<Q5_0>::codes(w[i], r.qh, i, lo, hi);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                q[4 * i + b] = ubyte(lo, b);
+                q[16 + 4 * i + b] = ubyte(hi, b);
+            }
+        }
+        A[0] = f16<EXACT>(r.dm & 0xFFFFu);
+        B[0] = f16<EXACT>(r.dm >> 16);
+    }
+    // q*d is exact (5 x 11 bits), so the fused form rounds like q*d + m.
+    __device__ static float value(float q, float A, float B) { return __builtin_fmaf(q, A, B); }
+};
+
+// -------------------------------------------------------------- IQ4_NL (18 B)
+// Block: d f16 @0, qs[16] @2; element j is T[nibble j % 16] (low for j < 16).
+template <>
+struct Fmt<IQ4_NL> {
+    static constexpr int BE = 32, BB = 18, NG = 1;
+    struct Raw {
+        uint32_t d;
+        uint4 qs;
+    };
+    __device__ static int k_of(int u, int s) { return 32 * u + s; }
+    template <bool NT = false>
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 18 * u;
+        return Raw{ldg16<NT>(p), ldg128<NT>(p + 2)};
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int, float* q, float* A, float* B) {
+        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = iq4_lookup(w[i]), hi = iq4_lookup(w[i] >> 4);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                q[4 * i + b] = (float)(int8_t)(lo >> (8 * b));
+                q[16 + 4 * i + b] = (float)(int8_t)(hi >> (8 * b));
+            }
+        }
+        A[0] = f16<EXACT>(r.d);
+        B[0] = 0.0f;
+    }
+    __device__ static float value(float q, float A, float) { return A * q; }
+};
+
+// --------------------------------------------------------------- Q3_K (110 B)
+// Super-block: hmask[32] @0, qs[64] @32, scales[12] @96, d f16 @108.  Element
+// 128 n + 32 j + l (l < 32): 2-bit code at bit 2 j of qs[32 n + l], plus 4
+// when bit 4 n + j of hmask[l] is set (the reference subtracts 4 when it is
+// clear), sub-scale 8 n + 2 j + l / 16 (matmul.cpp:284-338).  Unit
+// u = 4 n + c covers l in [8c, 8c+8) of half n: slot 8 j + e holds element
+// 128 n + 32 j + 8 c + e, group j, the same walk as Q6_K.
+template <>
+struct Fmt<Q3_K> {
+    static constexpr int BE = 256, BB = 110, NG = 4;
+    struct Raw {
+        uint2 qs, hm;
+        uint32_t s0, s1, s2, d;  // scale bytes 0-3, 4-7, 8-11; d
+    };
+    __device__ static int k_of(int u, int s) { return Fmt<Q6_K>::k_of(u, s); }
+    template <bool NT = false>
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 110 * (u >> 3);
+        const int j = u & 7, n = j >> 2, l0 = 8 * (j & 3);
+        return Raw{ldg64<NT>(p + 32 + 32 * n + l0), ldg64<NT>(p + l0), ldg32<NT>(p + 96),
+                   ldg32<NT>(p + 100), ldg32<NT>(p + 104), ldg16<NT>(p + 108)};
+    }
+    // Signed sub-scales of groups j = 0..3 of unit u: scale i = 8 n + 2 j + h
+    // (h = l >= 16) has its low nibble in nibble n of scale byte 2 j + h and
+    // its top 2 bits at bit 2 (2 n + j / 2) of byte 8 + (2 j + h) % 4.
+    __device__ static void scales(const Raw& r, int u, int (&sc)[4]) {
+        const int j = u & 7, n = j >> 2, h = (j & 3) >> 1;
+        const uint32_t a0 = r.s0 >> (8 * h), a1 = r.s1 >> (8 * h), b = r.s2 >> (8 * h);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t lo = ((g < 2 ? a0 : a1) >> (16 * (g & 1) + 4 * n)) & 15u;
+            const uint32_t hi = (b >> (16 * (g & 1) + 4 * n + 2 * (g >> 1))) & 3u;
+            sc[g] = (int)(lo | (hi << 4)) - 32;
+        }
+    }
+    // unsigned 3-bit codes (value + 4) of slots 8g + 4i .. +3
+    __device__ static uint32_t codes(const Raw& r, int u, int g, int i) {
+        const int n = (u & 7) >> 2;
+        const uint32_t q = i ? r.qs.y : r.qs.x, h = i ? r.hm.y : r.hm.x;
+        return ((q >> (2 * g)) & 0x03030303u) | (((h >> (4 * n + g)) & 0x01010101u) << 2);
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int u, float* q, float* A, float* B) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t c = codes(r, u, g, i);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) q[8 * g + 4 * i + e] = ubyte(c, e);
+            }
+        int sc[4];
+        scales(r, u, sc);
+        const float d = f16<EXACT>(r.d);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            A[g] = d * (float)sc[g];
+            B[g] = -4.0f * A[g];
+        }
+    }
+    __device__ static float value(float q, float A, float) { return A * (q - 4.0f); }
+};
+
+// --------------------------------------------------------------- Q5_K (176 B)
+// Super-block: d f16 @0, dmin f16 @2, scales[12] @4, qh[32] @16, qs[128] @48.
+// Element 64 g + 32 h + l: nibble h of qs[32 g + l] plus 16 times bit 2 g + h
+// of qh[l], scale/min pair 2 g + h (matmul.cpp:382-415).  Units as Q4_K:
+// unit j = 2 g + t reads qs[32 g + 16 t, +16) and qh[16 t, +16).
+template <>
+struct Fmt<Q5_K> {
+    static constexpr int BE = 256, BB = 176, NG = 2;
+    struct Raw {
+        uint4 hdr, qs, qh;
+    };
+    __device__ static int k_of(int u, int s) { return Fmt<Q4_K>::k_of(u, s); }
+    template <bool NT = false>
+    __device__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 176 * (u >> 3);
+        const int j = u & 7;
+        return Raw{ldg128<NT>(p), ldg128<NT>(p + 48 + 16 * j), ldg128<NT>(p + 16 + 16 * (j & 1))};
+    }
+    // 5-bit codes: slots 4i.. (low nibbles, bit 2g of qh) and 16+4i.. (bit 2g+1)
+    __device__ static void codes(const Raw& r, int u, int i, uint32_t& lo, uint32_t& hi) {
+        const int g = (u & 7) >> 1;
+        const uint32_t w = i == 0 ? r.qs.x : i == 1 ? r.qs.y : i == 2 ? r.qs.z : r.qs.w;
+        const uint32_t h = i == 0 ? r.qh.x : i == 1 ? r.qh.y : i == 2 ? r.qh.z : r.qh.w;
+        lo = (w & 0x0F0F0F0Fu) | (((h >> (2 * g)) & 0x01010101u) << 4);
+        hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (2 * g + 1)) & 0x01010101u) << 4);
+    }
+    template <bool EXACT>
+    __device__ static void decode(const Raw& r, int u, float* q, float* A, float* B) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo, hi;
+            codes(r, u, i, lo, hi);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                q[4 * i + b] = ubyte(lo, b);
+                q[16 + 4 * i + b] = ubyte(hi, b);
+            }
+        }
+        const float d = f16<EXACT>(r.hdr.x & 0xFFFFu), dmin = f16<EXACT>(r.hdr.x >> 16);
+        uint32_t sa, ma, sb, mb;
+        Fmt<Q4_K>::scale_min(r.hdr, (u & 7) >> 1, sa, ma, sb, mb);
+        A[0] = d * (float)sa;
+        B[0] = -(dmin * (float)ma);
+        A[1] = d * (float)sb;
+        B[1] = -(dmin * (float)mb);
+    }
+    // (d*sc)*q is exact (11 + 6 + 5 bits), so fma rounds like d1*q - m1.
+    __device__ static float value(float q, float A, float B) { return __builtin_fmaf(A, q, B); }
+};
+
 // ---------------------------------------------------------------- int8 limbs
 // Batch-1 path: the activations of one 32-slot unit are staged as three int8
 // limbs a1, a2, a3 (slot order, 4 slots per dword) and a power-of-two scale
@@ -461,6 +743,93 @@ __device__ __forceinline__ float limb_dot<Q6_K>(const Fmt<Q6_K>::Raw& r, int u, 
     const float d = f16_hw(r.d);
     // d * sum_g sc_g (P_g - 32 S_g)
     return d * __builtin_fmaf(L.s1, limb_sum(E[0], E[1], E[2]), -32.0f * sS);
+}
+
+// 5-bit nibble formats (Q5_0, Q5_1): one group; |sum| <= 32 * 127 * 31.
+template <class Fm>
+__device__ __forceinline__ void five_bit_dots(const uint4& qs, uint32_t qh, const Limbs& L,
+                                              int (&D)[3][1]) {
+    const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t lo, hi;
+        Fmt<Q5_0>::codes(w[i], qh, i, lo, hi);
+        acc_dword<1>((int)lo, i, L, D, 0);
+        acc_dword<1>((int)hi, 4 + i, L, D, 0);
+    }
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<Q5_0>(const Fmt<Q5_0>::Raw& r, int, const Limbs& L) {
+    int D[3][1] = {{0}, {0}, {0}};
+    five_bit_dots<Fmt<Q5_0>>(r.qs, r.qh, L, D);
+    const float d = f16_hw(r.d);
+    return __builtin_fmaf(d * L.s1, limb_sum(D[0][0], D[1][0], D[2][0]), -16.0f * d * L.S[0]);
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<Q5_1>(const Fmt<Q5_1>::Raw& r, int, const Limbs& L) {
+    int D[3][1] = {{0}, {0}, {0}};
+    five_bit_dots<Fmt<Q5_1>>(r.qs, r.qh, L, D);
+    const float d = f16_hw(r.dm & 0xFFFFu), m = f16_hw(r.dm >> 16);
+    return __builtin_fmaf(d * L.s1, limb_sum(D[0][0], D[1][0], D[2][0]), m * L.S[0]);
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<IQ4_NL>(const Fmt<IQ4_NL>::Raw& r, int, const Limbs& L) {
+    int D[3][1] = {{0}, {0}, {0}};
+    const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        acc_dword<1>((int)iq4_lookup(w[i]), i, L, D, 0);
+        acc_dword<1>((int)iq4_lookup(w[i] >> 4), 4 + i, L, D, 0);
+    }
+    return f16_hw(r.d) * L.s1 * limb_sum(D[0][0], D[1][0], D[2][0]);
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<Q3_K>(const Fmt<Q3_K>::Raw& r, int u, const Limbs& L) {
+    int D[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc_dword<4>((int)Fmt<Q3_K>::codes(r, u, g, i), 2 * g + i, L, D, g);
+    int sc[4];
+    Fmt<Q3_K>::scales(r, u, sc);
+    // sub-scales folded in integers: |sum_g sc_g D_g| <= 4 * 32 * 8 * 127 * 7
+    int E[3];
+    float sS = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+        int e = 0;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) e = __mul24(sc[g], D[l][g]) + e;
+        E[l] = e;
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sS = __builtin_fmaf((float)sc[g], L.S[g], sS);
+    // d * sum_g sc_g (P_g - 4 S_g), P_g over the unsigned codes
+    return f16_hw(r.d) * __builtin_fmaf(L.s1, limb_sum(E[0], E[1], E[2]), -4.0f * sS);
+}
+
+template <>
+__device__ __forceinline__ float limb_dot<Q5_K>(const Fmt<Q5_K>::Raw& r, int u, const Limbs& L) {
+    int D[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t lo, hi;
+        Fmt<Q5_K>::codes(r, u, i, lo, hi);
+        acc_dword<2>((int)lo, i, L, D, 0);
+        acc_dword<2>((int)hi, 4 + i, L, D, 1);
+    }
+    const float d = f16_hw(r.hdr.x & 0xFFFFu), dmin = f16_hw(r.hdr.x >> 16);
+    uint32_t sa, ma, sb, mb;
+    Fmt<Q4_K>::scale_min(r.hdr, (u & 7) >> 1, sa, ma, sb, mb);
+    const float ds = d * L.s1;
+    float acc = -(dmin * (float)ma) * L.S[0];
+    acc = __builtin_fmaf(-(dmin * (float)mb), L.S[1], acc);
+    acc = __builtin_fmaf(ds * (float)sa, limb_sum(D[0][0], D[1][0], D[2][0]), acc);
+    return __builtin_fmaf(ds * (float)sb, limb_sum(D[0][1], D[1][1], D[2][1]), acc);
 }
 
 }  // namespace fq

@@ -331,14 +331,8 @@ static const void* gemv1_fn(bool bias, int wg) {
 }
 
 const void* gemv1_kernel_fn(int dtype, bool bias, int wg) {
-    switch (dtype) {
-        case Q4_0: return gemv1_fn<Q4_0>(bias, wg);
-        case Q4_1: return gemv1_fn<Q4_1>(bias, wg);
-        case Q8_0: return gemv1_fn<Q8_0>(bias, wg);
-        case Q4_K: return gemv1_fn<Q4_K>(bias, wg);
-        case Q6_K: return gemv1_fn<Q6_K>(bias, wg);
-        default: return nullptr;
-    }
+    return with_format(dtype, (const void*)nullptr,
+                       [&](auto f) { return gemv1_fn<decltype(f)::value>(bias, wg); });
 }
 
 template <int F>
@@ -347,14 +341,7 @@ static size_t lds_of(int U, int wg) {
 }
 
 size_t gemv1_lds_bytes(int dtype, int U, int wg) {
-    switch (dtype) {
-        case Q4_0: return lds_of<Q4_0>(U, wg);
-        case Q4_1: return lds_of<Q4_1>(U, wg);
-        case Q8_0: return lds_of<Q8_0>(U, wg);
-        case Q4_K: return lds_of<Q4_K>(U, wg);
-        case Q6_K: return lds_of<Q6_K>(U, wg);
-        default: return 0;
-    }
+    return with_format(dtype, (size_t)0, [&](auto f) { return lds_of<decltype(f)::value>(U, wg); });
 }
 
 constexpr int WGR = 512;
@@ -395,14 +382,9 @@ const void* gemv1r_kernel_fn(int dtype, int U, int row_bytes, bool bias, int* np
     if (U > 128) return nullptr;
     const int nc = U > 64 ? 2 : 1;
     const int npr = (row_bytes + 16 + 1023) / 1024;
-    const void* fn = nullptr;
-    switch (dtype) {
-        case Q4_0: fn = rfn<Q4_0>(nc, npr, bias); break;
-        case Q4_1: fn = rfn<Q4_1>(nc, npr, bias); break;
-        case Q8_0: fn = rfn<Q8_0>(nc, npr, bias); break;
-        case Q4_K: fn = rfn<Q4_K>(nc, npr, bias); break;
-        case Q6_K: fn = rfn<Q6_K>(nc, npr, bias); break;
-    }
+    const void* fn = with_format(dtype, (const void*)nullptr, [&](auto f) {
+        return rfn<decltype(f)::value>(nc, npr, bias);
+    });
     if (!fn) return nullptr;
     *npr_out = npr;
     *lds_out = (size_t)U * RECB + (size_t)(WGR / 64) * npr * 1024;

@@ -56,8 +56,8 @@ __device__ __forceinline__ int slot_elem(int e) {
 
 template <int F>
 struct SubBlock {
-    static constexpr int SB = F == Q6_K ? 16 : 32;
-    static constexpr bool HAS_B = F == Q4_1 || F == Q4_K;
+    static constexpr int SB = F == Q6_K || F == Q3_K ? 16 : 32;
+    static constexpr bool HAS_B = F == Q4_1 || F == Q4_K || F == Q5_1 || F == Q5_K;
 };
 
 // ------------------------------------------------------------------ xprep
@@ -274,6 +274,148 @@ struct Task<Q6_K> {
             const uint32_t q6 = ((L[g] >> lsh) & 0x0F0F0F0Fu) | (((H[g] >> hsh) & 0x03030303u) << 4);
             h2 p0, p1;
             byte_pairs(q6, 0x00FF00FFu, (_Float16)1056.0f, p0, p1);
+            *reinterpret_cast<h4*>(dst + (16 * g + c) * 4) = h4{p0[0], p0[1], p1[0], p1[1]};
+        }
+    }
+};
+
+// Q5_0 / Q5_1: element e of a block is nibble e % 16 of qs (low for e < 16)
+// with bit e of qh as bit 4.  Lane group g holds elements 8g .. 8g+7.
+template <int OFF>
+__device__ __forceinline__ void put_five_bit(const fq_u32x4& q, uint32_t qh, int c, _Float16* dst) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int sh = g < 2 ? 0 : 4, i0 = 2 * (g & 1);
+        const uint32_t c0 = five_bit((w[i0] >> sh) & 0x0F0F0F0Fu, qh >> (8 * g));
+        const uint32_t c1 = five_bit((w[i0 + 1] >> sh) & 0x0F0F0F0Fu, qh >> (8 * g + 4));
+        *reinterpret_cast<h8*>(dst + (16 * g + c) * 8) = byte8(c0, c1, (_Float16)(float)OFF);
+    }
+}
+
+template <>
+struct Task<Q5_0> {  // block 2ch + s: d | qh | qs[16]
+    uint32_t d, qh;
+    fq_u32x4 q;
+    __device__ void load(const uint8_t* row, int ch, int s) {
+        const uint8_t* b = row + 22 * (2 * ch + s);
+        d = ld_u16(b);
+        qh = ld_u32(b + 2);
+        q = ldv(b + 6);
+    }
+    __device__ void put(int c, _Float16* dst, float& A, float& B) const {
+        A = f16_hw(d);
+        B = 0.0f;
+        put_five_bit<1040>(q, qh, c, dst);  // 1024 + 16
+    }
+};
+
+template <>
+struct Task<Q5_1> {  // block 2ch + s: d m | qh | qs[16]
+    uint32_t dm, qh;
+    fq_u32x4 q;
+    __device__ void load(const uint8_t* row, int ch, int s) {
+        const uint8_t* b = row + 24 * (2 * ch + s);
+        dm = ld_u32(b);
+        qh = ld_u32(b + 4);
+        q = ldv(b + 8);
+    }
+    __device__ void put(int c, _Float16* dst, float& A, float& B) const {
+        A = f16_hw(dm & 0xFFFFu);
+        B = f16_hw(dm >> 16);
+        put_five_bit<1024>(q, qh, c, dst);
+    }
+};
+
+template <>
+struct Task<IQ4_NL> {  // block 2ch + s: d | qs[16]; table values as int8
+    uint32_t d;
+    fq_u32x4 q;
+    __device__ void load(const uint8_t* row, int ch, int s) {
+        const uint8_t* b = row + 18 * (2 * ch + s);
+        d = ld_u16(b);
+        q = ldv(b + 2);
+    }
+    __device__ void put(int c, _Float16* dst, float& A, float& B) const {
+        A = f16_hw(d);
+        B = 0.0f;
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int sh = g < 2 ? 0 : 4, i0 = 2 * (g & 1);
+            const uint32_t v0 = iq4_lookup(w[i0] >> sh), v1 = iq4_lookup(w[i0 + 1] >> sh);
+            *reinterpret_cast<h8*>(dst + (16 * g + c) * 8) =
+                byte8(v0 ^ 0x80808080u, v1 ^ 0x80808080u, (_Float16)1152.0f);
+        }
+    }
+};
+
+template <>
+struct Task<Q5_K> {  // chunk ch = pair j of super-block ch / 4; s = 0 low, 1 high nibbles
+    fq_u32x4 hdr, q0, q1, h0, h1;
+    int j, s;
+    __device__ void load(const uint8_t* row, int ch, int s_) {
+        const uint8_t* sb = row + 176 * (ch >> 2);
+        j = ch & 3;
+        s = s_;
+        hdr = ldv(sb);
+        h0 = ldv(sb + 16);
+        h1 = ldv(sb + 32);
+        q0 = ldv(sb + 48 + 32 * j);
+        q1 = ldv(sb + 64 + 32 * j);
+    }
+    __device__ void put(int c, _Float16* dst, float& A, float& B) const {
+        uint32_t sa, ma, sb2, mb;
+        Fmt<Q4_K>::scale_min(uint4{hdr.x, hdr.y, hdr.z, hdr.w}, j, sa, ma, sb2, mb);
+        const float d = f16_hw(hdr.x & 0xFFFFu), dmin = f16_hw(hdr.x >> 16);
+        A = d * (float)(s ? sb2 : sa);
+        B = -(dmin * (float)(s ? mb : ma));
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        const int hb = 2 * j + s;  // qh bit of this sub-block
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t c0 = ((w[2 * g] >> (4 * s)) & 0x0F0F0F0Fu) |
+                                (((h[2 * g] >> hb) & 0x01010101u) << 4);
+            const uint32_t c1 = ((w[2 * g + 1] >> (4 * s)) & 0x0F0F0F0Fu) |
+                                (((h[2 * g + 1] >> hb) & 0x01010101u) << 4);
+            *reinterpret_cast<h8*>(dst + (16 * g + c) * 8) = byte8(c0, c1, (_Float16)1024.0f);
+        }
+    }
+};
+
+template <>
+struct Task<Q3_K> {
+    // chunk ch: super-block ch / 4, quarter qq = ch % 4 -> half n = qq / 2,
+    // rows j' = 2 (qq % 2) + {0, 1} of 32 elements 128 n + 32 j' + l.
+    // Sub-block s (16 elements): j' = 2 (qq % 2) + s / 2, l in [16 (s % 2), +16),
+    // sub-scale 8 n + 2 j' + s % 2 (matmul.cpp:284-338).
+    fq_u32x4 qs, hm;
+    uint32_t d, lo, hi;
+    int n, jp;
+    __device__ void load(const uint8_t* row, int ch, int s) {
+        const uint8_t* sb = row + 110 * (ch >> 2);
+        const int qq = ch & 3, l0 = 16 * (s & 1);
+        n = qq >> 1;
+        jp = 2 * (qq & 1) + (s >> 1);
+        const int i = 8 * n + 2 * jp + (s & 1);  // sub-scale index
+        d = ld_u16(sb + 108);
+        lo = sb[96 + (i & 7)] >> (4 * (i >> 3));
+        hi = sb[104 + (i & 3)] >> (2 * (i >> 2));
+        qs = ldv(sb + 32 + 32 * n + l0);
+        hm = ldv(sb + l0);
+    }
+    __device__ void put(int c, _Float16* dst, float& A, float& B) const {
+        A = f16_hw(d) * (float)((int)((lo & 15u) | ((hi & 3u) << 4)) - 32);
+        B = 0.0f;
+        const uint32_t Q[4] = {qs.x, qs.y, qs.z, qs.w};
+        const uint32_t H[4] = {hm.x, hm.y, hm.z, hm.w};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {  // elements l0 + 4g .. +4: codes + 4, then -4
+            const uint32_t q3 = ((Q[g] >> (2 * jp)) & 0x03030303u) |
+                                (((H[g] >> (4 * n + jp)) & 0x01010101u) << 2);
+            h2 p0, p1;
+            byte_pairs(q3, 0x00FF00FFu, (_Float16)1028.0f, p0, p1);
             *reinterpret_cast<h4*>(dst + (16 * g + c) * 4) = h4{p0[0], p0[1], p1[0], p1[1]};
         }
     }
@@ -539,7 +681,7 @@ void mmq_shape(int shape, int* bn, int* bm) {
 hipError_t launch_xprep(int dtype, const float* x, int M, int K, int NC, _Float16* xop,
                         float* xsum, int* ex, hipStream_t st) {
     const dim3 grid((M + 15) / 16, NC);
-    if (dtype == Q6_K)
+    if (dtype == Q6_K || dtype == Q3_K)
         hipLaunchKernelGGL(xprep_kernel<16>, grid, dim3(256), 0, st, x, M, K, NC, xop, xsum, ex);
     else
         hipLaunchKernelGGL(xprep_kernel<32>, grid, dim3(256), 0, st, x, M, K, NC, xop, xsum, ex);
@@ -548,14 +690,9 @@ hipError_t launch_xprep(int dtype, const float* x, int M, int K, int NC, _Float1
 
 hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, int splits,
                       hipStream_t st) {
-    hipError_t e = hipErrorInvalidValue;
-    switch (dtype) {
-        case Q4_0: e = launch_f<Q4_0>(a, shape, gx, gy, splits, st); break;
-        case Q4_1: e = launch_f<Q4_1>(a, shape, gx, gy, splits, st); break;
-        case Q8_0: e = launch_f<Q8_0>(a, shape, gx, gy, splits, st); break;
-        case Q4_K: e = launch_f<Q4_K>(a, shape, gx, gy, splits, st); break;
-        case Q6_K: e = launch_f<Q6_K>(a, shape, gx, gy, splits, st); break;
-    }
+    const hipError_t e = with_format(dtype, hipErrorInvalidValue, [&](auto f) {
+        return launch_f<decltype(f)::value>(a, shape, gx, gy, splits, st);
+    });
     if (e != hipSuccess || splits <= 1) return e;
     const size_t total = (size_t)a.M * a.N;
     const int grid = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);

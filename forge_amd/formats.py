@@ -2,8 +2,10 @@
 
 Mirrors forge::DataType (include/forge/types.h:7-26) and the block geometry of
 QuantTraits / data_type_traits (include/forge/quant_traits.h:19-95,
-src/operators/cpu/quant_traits.cpp:33-52) for the five formats this library
-implements.  The numeric dtype values are the reference's, so a caller can pass
+src/operators/cpu/quant_traits.cpp:33-52) for the ten formats this library
+implements: the five of the decode benchmarks (Q4_0, Q4_1, Q8_0, Q4_K, Q6_K)
+and the five other formats a Q4_K_M/Q5_K_M model file mixes in (Q5_0, Q5_1,
+Q3_K, Q5_K, IQ4_NL).  The numeric dtype values are the reference's, so a caller can pass
 ``static_cast<uint32_t>(tensor->dtype())`` straight through the C ABI.
 """
 from __future__ import annotations
@@ -15,7 +17,12 @@ Q4_0 = 2
 Q4_1 = 3
 Q4_K = 4
 Q8_0 = 7
+Q5_0 = 8
+Q5_1 = 9
+Q3_K = 11
+Q5_K = 12
 Q6_K = 13
+IQ4_NL = 17
 
 
 @dataclass(frozen=True)
@@ -42,7 +49,16 @@ FORMATS = {
     Q8_0: BlockFormat(Q8_0, "q8_0", 32, 34),
     Q4_K: BlockFormat(Q4_K, "q4_k", 256, 144),
     Q6_K: BlockFormat(Q6_K, "q6_k", 256, 210),
+    Q5_0: BlockFormat(Q5_0, "q5_0", 32, 22),
+    Q5_1: BlockFormat(Q5_1, "q5_1", 32, 24),
+    Q3_K: BlockFormat(Q3_K, "q3_k", 256, 110),
+    Q5_K: BlockFormat(Q5_K, "q5_k", 256, 176),
+    IQ4_NL: BlockFormat(IQ4_NL, "iq4_nl", 32, 18),
 }
+
+# Formats with an aligned (repacked) device layout; the others run from
+# their GGUF bytes only.
+PACKED = (Q4_0, Q4_1, Q8_0, Q4_K, Q6_K)
 
 BY_NAME = {f.name: f for f in FORMATS.values()}
 

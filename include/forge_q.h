@@ -9,7 +9,9 @@
  *
  * Conventions (shared by all entry points)
  *  - dtype: a forge::DataType value (include/forge/types.h:7-26 of the
- *    reference): Q4_0=2, Q4_1=3, Q4_K=4, Q8_0=7, Q6_K=13.
+ *    reference): Q4_0=2, Q4_1=3, Q4_K=4, Q8_0=7, Q5_0=8, Q5_1=9, Q3_K=11,
+ *    Q5_K=12, Q6_K=13, IQ4_NL=17.  The packed (aligned) layout exists for
+ *    Q4_0, Q4_1, Q8_0, Q4_K and Q6_K only.
  *  - w: device pointer to a row-major [N][K/block_elems] array of on-disk
  *    GGUF blocks, rows contiguous with no padding (the layout
  *    forge::compute_quantized_bytes sizes, quant_traits.h:138-146).  No
@@ -37,7 +39,7 @@ extern "C" {
 #endif
 
 #define FQ_OK 0
-#define FQ_ERR_DTYPE 1    /* dtype is not one of the five block formats          */
+#define FQ_ERR_DTYPE 1    /* dtype is not one of the ten block formats           */
 #define FQ_ERR_SHAPE 2    /* M/N/K out of range or K not a multiple of the block  */
 #define FQ_ERR_NULL 3     /* a required pointer is NULL                           */
 #define FQ_ERR_HIP 4      /* the HIP runtime reported an error (fq_last_hip_error) */
@@ -49,7 +51,12 @@ extern "C" {
 #define FQ_DTYPE_Q4_1 3u
 #define FQ_DTYPE_Q4_K 4u
 #define FQ_DTYPE_Q8_0 7u
+#define FQ_DTYPE_Q5_0 8u
+#define FQ_DTYPE_Q5_1 9u
+#define FQ_DTYPE_Q3_K 11u
+#define FQ_DTYPE_Q5_K 12u
 #define FQ_DTYPE_Q6_K 13u
+#define FQ_DTYPE_IQ4_NL 17u
 
 /* Block geometry of a dtype: elements and bytes per block.
  * Replaces data_type_traits[] lookups (src/operators/cpu/quant_traits.cpp:33-52,

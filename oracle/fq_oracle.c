@@ -23,6 +23,11 @@ int fqo_block_info(uint32_t dtype, int* block_elems, int* block_bytes) {
         case FQO_Q8_0: e = 32;  b = 34;  break;
         case FQO_Q4_K: e = 256; b = 144; break;
         case FQO_Q6_K: e = 256; b = 210; break;
+        case FQO_Q5_0: e = 32;  b = 22;  break;
+        case FQO_Q5_1: e = 32;  b = 24;  break;
+        case FQO_Q3_K: e = 256; b = 110; break;
+        case FQO_Q5_K: e = 256; b = 176; break;
+        case FQO_IQ4_NL: e = 32; b = 18; break;
         default: return -1;
     }
     if (block_elems) *block_elems = e;
@@ -167,6 +172,117 @@ static void deq_q6_k_row(const uint8_t* row, float* out, int K) {
     }
 }
 
+static uint32_t rd32(const uint8_t* p) {
+    uint32_t v;
+    memcpy(&v, p, 4);
+    return v;
+}
+
+/* matmul.cpp:125-152.  Element j (j < 32) of a block: 4 low bits from the
+ * nibble j % 16 of qs (low nibble for j < 16), bit 4 from bit j of qh. */
+static void deq_q5_0_row(const uint8_t* row, float* out, int K) {
+    int nb = (K + 31) / 32;
+    for (int bi = 0; bi < nb; ++bi) {
+        const uint8_t* blk = row + (size_t)bi * 22;
+        float d = fqo_fp16_to_fp32(rd16(blk));
+        uint32_t qh = rd32(blk + 2);
+        const uint8_t* qs = blk + 6;
+        for (int j = 0; j < 32 && bi * 32 + j < K; ++j) {
+            int lo4 = j < 16 ? (qs[j] & 0x0F) : (qs[j - 16] >> 4);
+            int q = lo4 | (int)(((qh >> j) & 1u) << 4);
+            out[bi * 32 + j] = (float)(q - 16) * d;
+        }
+    }
+}
+
+/* matmul.cpp:156-186: the same 5-bit codes, w = q * d + m. */
+static void deq_q5_1_row(const uint8_t* row, float* out, int K) {
+    int nb = (K + 31) / 32;
+    for (int bi = 0; bi < nb; ++bi) {
+        const uint8_t* blk = row + (size_t)bi * 24;
+        float d = fqo_fp16_to_fp32(rd16(blk));
+        float m = fqo_fp16_to_fp32(rd16(blk + 2));
+        uint32_t qh = rd32(blk + 4);
+        const uint8_t* qs = blk + 8;
+        for (int j = 0; j < 32 && bi * 32 + j < K; ++j) {
+            int lo4 = j < 16 ? (qs[j] & 0x0F) : (qs[j - 16] >> 4);
+            int q = lo4 | (int)(((qh >> j) & 1u) << 4);
+            out[bi * 32 + j] = (float)q * d + m;
+        }
+    }
+}
+
+/* matmul.cpp:284-338.  The 16 six-bit scales of a super-block: scale i has
+ * its low 4 bits in nibble (i >> 3) of byte (i & 7) and its high 2 bits in
+ * bits 2 (i >> 2) .. +1 of byte 8 + (i & 3); the value used is scale - 32. */
+static int q3_k_scale(const uint8_t* raw, int i) {
+    int lo4 = (raw[i & 7] >> (4 * (i >> 3))) & 0xF;
+    int hi2 = (raw[8 + (i & 3)] >> (2 * (i >> 2))) & 3;
+    return (lo4 | (hi2 << 4)) - 32;
+}
+
+/* matmul.cpp:284-338.  Element e = 128 n + 32 j + l of a super-block
+ * (n < 2, j < 4, l < 32): 2 low bits at bit 2 j of qs[32 n + l], minus 4
+ * unless bit 4 n + j of hmask[l] is set; scale 8 n + 2 j + l / 16. */
+static void deq_q3_k_row(const uint8_t* row, float* out, int K) {
+    int nb = (K + 255) / 256;
+    for (int bi = 0; bi < nb; ++bi) {
+        const uint8_t* blk = row + (size_t)bi * 110;
+        const uint8_t* hm = blk;
+        const uint8_t* qs = blk + 32;
+        const uint8_t* sc = blk + 96;
+        float d = fqo_fp16_to_fp32(rd16(blk + 108));
+        for (int e = 0; e < 256 && bi * 256 + e < K; ++e) {
+            int n = e / 128, j = (e % 128) / 32, l = e % 32;
+            int q = (qs[32 * n + l] >> (2 * j)) & 3;
+            if (!((hm[l] >> (4 * n + j)) & 1)) q -= 4;
+            float dl = d * (float)q3_k_scale(sc, 8 * n + 2 * j + l / 16);
+            out[bi * 256 + e] = dl * (float)q;
+        }
+    }
+}
+
+/* matmul.cpp:382-415.  Element 64 g + 32 h + l (g < 4, h < 2, l < 32):
+ * nibble h of qs[32 g + l] plus 16 times bit 2 g + h of qh[l], scale/min
+ * pair 2 g + h (get_scale_min_k4, as Q4_K). */
+static void deq_q5_k_row(const uint8_t* row, float* out, int K) {
+    int nb = (K + 255) / 256;
+    for (int bi = 0; bi < nb; ++bi) {
+        const uint8_t* blk = row + (size_t)bi * 176;
+        float d = fqo_fp16_to_fp32(rd16(blk));
+        float dmin = fqo_fp16_to_fp32(rd16(blk + 2));
+        const uint8_t* scales = blk + 4;
+        const uint8_t* qh = blk + 16;
+        const uint8_t* qs = blk + 48;
+        for (int e = 0; e < 256 && bi * 256 + e < K; ++e) {
+            int g = e / 64, h = (e % 64) / 32, l = e % 32;
+            uint8_t sc, m;
+            scale_min_k4(2 * g + h, scales, &sc, &m);
+            int q = ((qs[32 * g + l] >> (4 * h)) & 0xF) + (((qh[l] >> (2 * g + h)) & 1) ? 16 : 0);
+            float d1 = d * (float)sc;
+            float m1 = dmin * (float)m;
+            out[bi * 256 + e] = d1 * (float)q - m1;
+        }
+    }
+}
+
+/* matmul.cpp:849-868: 4-bit indices into a fixed non-linear table. */
+static const int8_t iq4nl_values[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                        1,    13,   25,  38,  53,  69,  89,  113};
+
+static void deq_iq4_nl_row(const uint8_t* row, float* out, int K) {
+    int nb = (K + 31) / 32;
+    for (int bi = 0; bi < nb; ++bi) {
+        const uint8_t* blk = row + (size_t)bi * 18;
+        float d = fqo_fp16_to_fp32(rd16(blk));
+        const uint8_t* qs = blk + 2;
+        for (int j = 0; j < 32 && bi * 32 + j < K; ++j) {
+            int idx = j < 16 ? (qs[j] & 0x0F) : (qs[j - 16] >> 4);
+            out[bi * 32 + j] = d * (float)iq4nl_values[idx];
+        }
+    }
+}
+
 typedef void (*deq_fn)(const uint8_t*, float*, int);
 
 static deq_fn pick(uint32_t dtype) {
@@ -176,6 +292,11 @@ static deq_fn pick(uint32_t dtype) {
         case FQO_Q8_0: return deq_q8_0_row;
         case FQO_Q4_K: return deq_q4_k_row;
         case FQO_Q6_K: return deq_q6_k_row;
+        case FQO_Q5_0: return deq_q5_0_row;
+        case FQO_Q5_1: return deq_q5_1_row;
+        case FQO_Q3_K: return deq_q3_k_row;
+        case FQO_Q5_K: return deq_q5_k_row;
+        case FQO_IQ4_NL: return deq_iq4_nl_row;
         default: return NULL;
     }
 }

@@ -30,11 +30,16 @@ enum {
     FQO_Q4_1 = 3,
     FQO_Q4_K = 4,
     FQO_Q8_0 = 7,
+    FQO_Q5_0 = 8,
+    FQO_Q5_1 = 9,
+    FQO_Q3_K = 11,
+    FQO_Q5_K = 12,
     FQO_Q6_K = 13,
+    FQO_IQ4_NL = 17,
 };
 
 /* Block geometry, include/forge/quant_traits.h:19-95.  Returns 0 on success,
- * -1 for a dtype outside the five formats of the hot path. */
+ * -1 for a dtype outside the ten formats of the hot path. */
 int fqo_block_info(uint32_t dtype, int* block_elems, int* block_bytes);
 
 /* IEEE binary16 -> binary32, exact incl. subnormals.
@@ -50,8 +55,13 @@ float fqo_fp16_to_fp32(uint16_t bits);
  *   get_scale_min_k4     matmul.cpp:232-240
  *   dequantize_q6_k_row  matmul.cpp:242-279
  *   dequantize_q4_k_row  matmul.cpp:340-377
- * Only the first K values of each row are written (the reference's Q6_K row
- * routine writes whole 256-element super-blocks even past K).
+ *   dequantize_q5_0_row  matmul.cpp:125-152
+ *   dequantize_q5_1_row  matmul.cpp:156-186
+ *   dequantize_q3_k_row  matmul.cpp:284-338
+ *   dequantize_q5_k_row  matmul.cpp:382-415
+ *   dequantize_iq4_nl_row matmul.cpp:849-868
+ * Only the first K values of each row are written (the reference's Q6_K, Q3_K,
+ * Q5_K and IQ4_NL row routines write whole blocks even past K).
  * Pinned: golden + closed form (independent encoder round trip).
  * Returns 0, or -1 for an unsupported dtype / bad shape. */
 int fqo_dequant_rows(uint32_t dtype, const uint8_t* w, float* out, int N, int K);

@@ -6,7 +6,7 @@ inputs and stores inputs and outputs as small .npz fixtures beside this
 script.  The fixtures are data: block bytes, activations, the reference's
 dequantized rows and the reference's ops::matmul_transB outputs.
 
-Usage:  python tests/golden/gen_golden.py
+Usage:  python tests/golden/gen_golden.py [format ...]   (default: all)
 """
 from __future__ import annotations
 
@@ -34,6 +34,12 @@ FINITE_F16 = [h for h in SPECIAL_F16 if (h & 0x7C00) != 0x7C00]
 
 SCALE_OFFSETS = {  # byte offsets of fp16 fields inside a block
     F.Q4_0: [0], F.Q4_1: [0, 2], F.Q8_0: [0], F.Q4_K: [0, 2], F.Q6_K: [208],
+    F.Q5_0: [0], F.Q5_1: [0, 2], F.Q3_K: [108], F.Q5_K: [0, 2], F.IQ4_NL: [0],
+}
+# byte range [lo, hi) of the quant payload (everything but the fp16 fields)
+PAYLOAD = {
+    F.Q4_0: (2, 18), F.Q4_1: (4, 20), F.Q8_0: (2, 34), F.Q4_K: (4, 144), F.Q6_K: (0, 208),
+    F.Q5_0: (2, 22), F.Q5_1: (4, 24), F.Q3_K: (0, 108), F.Q5_K: (4, 176), F.IQ4_NL: (2, 18),
 }
 
 
@@ -75,8 +81,7 @@ def extreme_payload(w, f, K):
     """Saturate the quant payload of every other row (all-0 / all-1 bits)."""
     nb = -(-K // f.block_elems)
     blk = w.reshape(w.shape[0], nb, f.block_bytes)
-    lo = {F.Q4_0: 2, F.Q4_1: 4, F.Q8_0: 2, F.Q4_K: 4, F.Q6_K: 0}[f.dtype]
-    hi = {F.Q4_0: 18, F.Q4_1: 20, F.Q8_0: 34, F.Q4_K: 144, F.Q6_K: 208}[f.dtype]
+    lo, hi = PAYLOAD[f.dtype]
     blk[0::4, :, lo:hi] = 0x00
     blk[1::4, :, lo:hi] = 0xFF
     if f.dtype == F.Q8_0:
@@ -86,7 +91,10 @@ def extreme_payload(w, f, K):
 
 def main():
     L = lib()
+    only = {F.fmt(a).dtype for a in sys.argv[1:]}
     for dt, f in F.FORMATS.items():
+        if only and dt not in only:
+            continue
         cases = {}
         K = 512 if f.block_elems == 32 else 1024
         N = 7  # not a multiple of the reference's 4-row decode tile

@@ -39,7 +39,8 @@ def test_block_info_matches_reference_traits():
         assert L.fq_block_info(dt, ctypes.byref(e), ctypes.byref(b)) == 0
         assert (e.value, b.value) == (f.block_elems, f.block_bytes)
     assert L.fq_block_info(0, None, None) == _lib.FQ_ERR_DTYPE  # FP32 is not a block format
-    assert L.fq_block_info(12, None, None) == _lib.FQ_ERR_DTYPE  # Q5_K not implemented
+    assert L.fq_block_info(10, None, None) == _lib.FQ_ERR_DTYPE  # Q2_K not implemented
+    assert L.fq_block_info(16, None, None) == _lib.FQ_ERR_DTYPE  # IQ2_XXS not implemented
 
 
 def test_status_strings():
@@ -89,6 +90,12 @@ def test_packed_row_bytes():
     L = _lib.lib()
     # same bytes as the GGUF row (plus at most 15 bytes of row padding)
     for dt, f in F.FORMATS.items():
+        if dt not in F.PACKED:  # GGUF layout only
+            assert L.fq_packed_row_bytes(dt, 256) == 0
+            one = ctypes.c_void_p(16)
+            assert L.fq_pack_weights(dt, one, one, 1, 256, None) == _lib.FQ_ERR_DTYPE
+            assert L.fq_gemv_packed(dt, one, one, None, 0, one, 256, 1, None) == _lib.FQ_ERR_DTYPE
+            continue
         for K in (256, 2048, 3584, 18944):
             pb = L.fq_packed_row_bytes(dt, K)
             assert pb % 16 == 0

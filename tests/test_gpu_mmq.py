@@ -39,7 +39,7 @@ def test_token_counts(dtype, M):
     check(dtype, N, K, x, seed=7 * M + dtype, what=f"{F.fmt(dtype).name} M={M}")
 
 
-@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0])
+@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q5_0, F.Q5_1, F.IQ4_NL])
 @pytest.mark.parametrize("K", [32, 96, 160, 4128])
 def test_half_chunk_tail(dtype, K):
     # K % 64 == 32: the last chunk holds one 32-element block

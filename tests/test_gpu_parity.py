@@ -22,7 +22,7 @@ from helpers import assert_close, golden_files, load_golden
 
 pytestmark = pytest.mark.gpu
 
-ALL = [F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K]
+ALL = sorted(F.FORMATS)
 DEV = "cuda"
 
 
@@ -120,7 +120,8 @@ def test_small_batch_config3(M):
     check_shape(F.Q4_K, 14336, 4096, M, seed=3000 + M, what=f"cfg3 M={M}")
 
 
-@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q6_K])
+@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q6_K, F.Q5_0, F.Q5_1, F.Q3_K,
+                                   F.Q5_K, F.IQ4_NL])
 @pytest.mark.parametrize("M", [2, 5, 16])
 def test_small_batch_formats(dtype, M):
     check_shape(dtype, 1000, 2048 if F.fmt(dtype).block_elems == 32 else 2560, M, seed=M + dtype)
@@ -151,7 +152,9 @@ def test_prefill_config4(dtype, N):
 def test_onehot_pins_unpack_through_gemv(dtype):
     """x = e_k selects column k of W.  For every format but Q6_K the kernel's
     arithmetic on a one-hot x is exact, so y must equal the dequantized
-    column bit for bit; Q6_K's offset term rounds once more (tolerance)."""
+    column bit for bit (up to the sign of zero: Q3_K's signed scales give the
+    reference -0 where the kernel's sum gives +0); Q6_K's offset term rounds
+    once more (tolerance)."""
     N, K = 96, 4096
     w = synth.make_weights(dtype, N, K, seed=55 + dtype)
     deq = oracle.dequant(dtype, w, N, K)
@@ -164,7 +167,8 @@ def test_onehot_pins_unpack_through_gemv(dtype):
             # the offset term adds one rounding of (d*sc)*(q+32) before - 32*d*sc
             np.testing.assert_allclose(y, deq[:, k], rtol=0, atol=4e-6 * np.abs(deq).max())
         else:
-            assert np.array_equal(y.view(np.uint32), deq[:, k].view(np.uint32)), k
+            want = deq[:, k] + np.float32(0.0)  # -0 -> +0
+            assert np.array_equal((y + np.float32(0.0)).view(np.uint32), want.view(np.uint32)), k
 
 
 @pytest.mark.parametrize("dtype", ALL)
@@ -222,7 +226,7 @@ def test_operator_errors():
         ops.matmul_transB(torch.zeros((1, 32), device=DEV), W)
     with pytest.raises(RuntimeError, match="expects 2D"):
         ops.matmul_transB(torch.zeros((64,), device=DEV), W)
-    bad = ops.QWeight(W.data, 12, 8, 64)  # Q5_K: not implemented on this path
+    bad = ops.QWeight(W.data, 10, 8, 64)  # Q2_K: not implemented on this path
     with pytest.raises(RuntimeError, match="Unsupported quantized type"):
         ops.matmul_transB(torch.zeros((1, 64), device=DEV), bad)
 

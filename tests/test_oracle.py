@@ -20,7 +20,11 @@ from forge_amd import formats as F
 from forge_amd import synth
 from helpers import assert_close, golden_files, load_golden
 
-ALL = [F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K]
+ALL = sorted(F.FORMATS)
+
+# IQ4_NL code -> value table of the format definition (matmul.cpp:849-851)
+IQ4_NL_VALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10,
+                          1, 13, 25, 38, 53, 69, 89, 113], np.float32)
 
 
 # ---------------------------------------------------------------- fp16
@@ -134,6 +138,67 @@ def encode(dtype, codes, d, extra=None):
         out[..., 208:210] = dh.view(np.uint8).reshape(N, nb, 2)
         dsc = df * sc[..., e // 16].astype(np.float32)  # element e -> sub-block e // 16
         want = dsc * (c.astype(np.float32) - 32.0)
+    elif dtype in (F.Q5_0, F.Q5_1):
+        qs_off = 6 if dtype == F.Q5_0 else 8
+        out[..., 0:2] = dh.view(np.uint8).reshape(N, nb, 2)
+        out[..., qs_off:qs_off + 16] = ((c[..., :16] & 15) | ((c[..., 16:] & 15) << 4)).astype(np.uint8)
+        qh = np.zeros((N, nb), np.uint64)
+        for j in range(32):  # bit j of the 32-bit qh word is bit 4 of element j
+            qh |= ((c[..., j] >> 4) & 1).astype(np.uint64) << np.uint64(j)
+        out[..., qs_off - 4:qs_off] = qh.astype("<u4").view(np.uint8).reshape(N, nb, 4)
+        if dtype == F.Q5_0:
+            want = (c.astype(np.float32) - 16.0) * df
+        else:
+            mh = _f16(extra).reshape(N, nb)
+            out[..., 2:4] = mh.view(np.uint8).reshape(N, nb, 2)
+            want = c.astype(np.float32) * df + mh.astype(np.float32)[..., None]
+    elif dtype == F.IQ4_NL:
+        out[..., 0:2] = dh.view(np.uint8).reshape(N, nb, 2)
+        out[..., 2:18] = (c[..., :16] | (c[..., 16:] << 4)).astype(np.uint8)
+        want = df * IQ4_NL_VALUES[c]
+    elif dtype == F.Q3_K:
+        sc = extra["sc"]  # [N, nb, 16] in -32..31
+        hm = np.zeros((N, nb, 32), np.int64)
+        qs = np.zeros((N, nb, 64), np.int64)
+        for e in range(256):  # 128-element halves, 32-element rows of 2-bit planes
+            n, j, l = e // 128, (e % 128) // 32, e % 32
+            qs[..., 32 * n + l] |= (c[..., e] & 3) << (2 * j)  # c in -4..3, two's complement
+            hm[..., l] |= (c[..., e] >= 0).astype(np.int64) << (4 * n + j)
+        raw = np.zeros((N, nb, 12), np.int64)
+        for j in range(16):  # scale j + 32 as 6 bits: low nibbles, then 2-bit high parts
+            v = sc[..., j] + 32
+            if j < 8:
+                raw[..., j] |= v & 15
+            else:
+                raw[..., j - 8] |= (v & 15) << 4
+            raw[..., 8 + j % 4] |= (v >> 4) << (2 * (j // 4))
+        out[..., 0:32] = hm.astype(np.uint8)
+        out[..., 32:96] = qs.astype(np.uint8)
+        out[..., 96:108] = raw.astype(np.uint8)
+        out[..., 108:110] = dh.view(np.uint8).reshape(N, nb, 2)
+        dl = df * sc[..., np.arange(256) // 16].astype(np.float32)  # 16-element sub-blocks
+        want = dl * c.astype(np.float32)
+    elif dtype == F.Q5_K:
+        dmin_h = _f16(extra["dmin"]).reshape(N, nb)
+        sc, mn = extra["sc"], extra["m"]
+        out[..., 0:2] = dh.view(np.uint8).reshape(N, nb, 2)
+        out[..., 2:4] = dmin_h.view(np.uint8).reshape(N, nb, 2)
+        s = np.zeros((N, nb, 12), np.uint16)
+        s[..., 0:4] = (sc[..., 0:4] & 63) | ((sc[..., 4:8] >> 4) << 6)
+        s[..., 4:8] = (mn[..., 0:4] & 63) | ((mn[..., 4:8] >> 4) << 6)
+        s[..., 8:12] = (sc[..., 4:8] & 15) | ((mn[..., 4:8] & 15) << 4)
+        out[..., 4:16] = s.astype(np.uint8)
+        cc = c.reshape(N, nb, 4, 2, 32)  # [.., pair g, sub 0/1, 32]
+        out[..., 48:176] = ((cc[..., 0, :] & 15) | ((cc[..., 1, :] & 15) << 4)).reshape(N, nb, 128)
+        qh = np.zeros((N, nb, 32), np.int64)
+        for g in range(4):
+            for h in range(2):
+                qh |= ((cc[..., g, h, :] >> 4) & 1) << (2 * g + h)
+        out[..., 16:48] = qh.astype(np.uint8)
+        sub = np.repeat(np.arange(8), 32)
+        d1 = df * sc[..., sub].astype(np.float32)
+        m1 = dmin_h.astype(np.float32)[..., None] * mn[..., sub].astype(np.float32)
+        want = d1 * c.astype(np.float32) - m1
     return out.reshape(N, -1), want.reshape(N, K).astype(np.float32)
 
 
@@ -142,15 +207,21 @@ def random_codes(dtype, N, K, rng):
     nb = K // f.block_elems
     d = np.abs(rng.normal(0, 0.05, size=(N, nb)))
     extra = None
-    if dtype in (F.Q4_0, F.Q4_1, F.Q4_K):
+    if dtype in (F.Q4_0, F.Q4_1, F.Q4_K, F.IQ4_NL):
         codes = rng.integers(0, 16, size=(N, K))
     elif dtype == F.Q8_0:
         codes = rng.integers(-128, 128, size=(N, K))
+    elif dtype in (F.Q5_0, F.Q5_1, F.Q5_K):
+        codes = rng.integers(0, 32, size=(N, K))
+    elif dtype == F.Q3_K:
+        codes = rng.integers(-4, 4, size=(N, K))
     else:
         codes = rng.integers(0, 64, size=(N, K))
-    if dtype == F.Q4_1:
+    if dtype in (F.Q4_1, F.Q5_1):
         extra = rng.normal(0, 0.3, size=(N, nb))
-    elif dtype == F.Q4_K:
+    elif dtype == F.Q3_K:
+        extra = dict(sc=rng.integers(-32, 32, size=(N, nb, 16)))
+    elif dtype in (F.Q4_K, F.Q5_K):
         extra = dict(dmin=np.abs(rng.normal(0, 0.05, size=(N, nb))),
                      sc=rng.integers(0, 64, size=(N, nb, 8)),
                      m=rng.integers(0, 64, size=(N, nb, 8)))
