@@ -417,6 +417,10 @@ def all_configs():
         for N in (4096, 14336):
             lines.append(time_config(f"cfg4-{'q8_0' if dt == Q8_0 else 'q4_0'}", dt, N, 4096, 512,
                                      reps=10))
+    # the formats outside the benchmark configs, at the 7B gate shape (GGUF layout)
+    for name, dt in (("q5_0", 8), ("q5_1", 9), ("q3_k", 11), ("q5_k", 12), ("iq4_nl", 17)):
+        for M in (1, 8):
+            lines.append(time_config(f"fmt-{name}", dt, 18944, 3584, M))
     return lines
 
 
