@@ -211,7 +211,40 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         }
     }
 
-    // M > 1, and M == 1 rows too long for the batch-1 kernels' LDS
+    if (M >= 2 && M <= 4 && K > 0) {
+        // a few tokens: the batch-1 chunk kernel reads and unpacks each weight
+        // unit once and dots it with every token's activation limbs
+        const int U1 = K / 32;
+        size_t lds = 0;
+        const void* fn = fq::gemv1_multi_fn((int)dtype, bias_mode != 0, M, &lds, U1);
+        if (fn && lds <= std::min<size_t>(di.lds, 160 * 1024)) {
+            int per_cu = 0;
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 1024, lds);
+            if (e != hipSuccess) return hip_fail(e);
+            if (per_cu >= 1) {
+                fq::GemvArgs a{};
+                a.x = x;
+                a.w = static_cast<const uint8_t*>(w);
+                a.y = y;
+                a.bias = bias;
+                a.bias_len = bias_mode == 0 ? 0 : bias_len;
+                a.bias_mode = bias_mode;
+                a.M = M;
+                a.K = K;
+                a.N = N;
+                a.U = U1;
+                a.Uc = U1;
+                a.row_bytes = (K / g.be) * g.bb;
+                const long waves = (long)di.cus * per_cu * 16;
+                const long need = std::min<long>(waves, N);
+                const int grid = (int)std::max(1L, (need + 15) / 16);
+                e = fq::launch_raw(fn, a, grid, 1024, lds, st);
+                return e == hipSuccess ? FQ_OK : hip_fail(e);
+            }
+        }
+    }
+
+    // M > 4, and rows too long for the batch-1 kernels' LDS
     return run_mmq(dtype, g, x, w, bias, bias_mode, bias_len, y, M, K, N, dev, di, st);
 }
 

@@ -122,44 +122,54 @@ __device__ __forceinline__ void spill(const Fetch<F>& f, uint8_t* wbuf, int lane
 // selects) and no stores: a store or a branch between the fetches would sit
 // in the same in-order counter as the weight loads and make the compiler
 // drain every load in flight, collapsing the two-deep pipeline.
-template <int F, bool BIAS>
+// NT tokens: the unit's weights are read and unpacked once and dotted with
+// each token's limb records (token m's records start at lds + m U RECB).
+template <int F, bool BIAS, int NT>
 __device__ __forceinline__ void consume(const GemvArgs& a, const Pos& p, const uint8_t* wbuf,
-                                        const uint8_t* lds, int lane, int nc, float& acc,
-                                        float& res, int& k) {
+                                        const uint8_t* lds, int lane, int nc, float (&acc)[NT],
+                                        float (&res)[NT], int& k) {
     const int shift = (int)(reinterpret_cast<uintptr_t>(chunk_addr<F>(a, p)) & 15);
     const int nunits = min(64, a.U - 64 * p.c);
     const int ul = min(lane, nunits - 1);
     const auto raw = Fmt<F>::template load<false>(wbuf + shift, ul);
-    const float t = unit_dot1<F>(raw, 64 * p.c + ul, lds, acc);
-    acc = lane < nunits ? t : acc;
     const bool row_end = p.c == nc - 1;  // wave-uniform
-    float s = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
-    if constexpr (BIAS) {
-        const int r = min(p.row, a.N - 1);
-        s += r < a.bias_len ? ((const_fp)(uintptr_t)a.bias)[r] : 0.0f;
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+        const float t = unit_dot1<F>(raw, 64 * p.c + ul, lds + (size_t)m * a.U * RECB, acc[m]);
+        acc[m] = lane < nunits ? t : acc[m];
+        float s = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc[m])), 63));
+        if constexpr (BIAS) {
+            const int r = min(p.row, a.N - 1);
+            if (a.bias_mode == 2)
+                s += ((const_fp)(uintptr_t)a.bias)[(size_t)m * a.N + r];
+            else
+                s += r < a.bias_len ? ((const_fp)(uintptr_t)a.bias)[r] : 0.0f;
+        }
+        res[m] = (row_end && lane == k) ? s : res[m];
+        acc[m] = row_end ? 0.0f : acc[m];
     }
-    res = (row_end && lane == k) ? s : res;
     k += row_end ? 1 : 0;
-    acc = row_end ? 0.0f : acc;
 }
 
-template <int F, bool BIAS>
+template <int F, bool BIAS, int NT>
 __device__ __forceinline__ void step(Fetch<F>& f, Pos& ld, Pos& cp, const GemvArgs& a,
                                      uint8_t* wbuf, const uint8_t* lds, int lane, int nc,
-                                     int stride, float& acc, float& res, int& k) {
+                                     int stride, float (&acc)[NT], float (&res)[NT], int& k) {
     // sched_barrier keeps the scheduler from hoisting the next step's spill
     // (and the wait for its loads) above this step's fetch
     __builtin_amdgcn_sched_barrier(0);
     spill<F>(f, wbuf, lane);
     fetch<F>(f, a, ld, lane);
     ld.next(nc, stride);
-    consume<F, BIAS>(a, cp, wbuf, lds, lane, nc, acc, res, k);
+    consume<F, BIAS, NT>(a, cp, wbuf, lds, lane, nc, acc, res, k);
     cp.next(nc, stride);
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int F, bool BIAS, int WG1>
+// NT tokens (a.M == NT) share each weight fetch; records of all NT tokens
+// are staged.
+template <int F, bool BIAS, int WG1, int NT = 1>
 __global__ __launch_bounds__(WG1) void gemv1_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -167,21 +177,23 @@ __global__ __launch_bounds__(WG1) void gemv1_kernel(GemvArgs a) {
     const int stride = gridDim.x * (WG1 / 64);
     const int first = __builtin_amdgcn_readfirstlane(blockIdx.x * (WG1 / 64) + wave);
     const int nc = (a.U + 63) >> 6;
-    uint8_t* wbuf = lds + (size_t)a.U * RECB + wave * Chunk<F>::WBUF;
+    uint8_t* wbuf = lds + (size_t)NT * a.U * RECB + wave * Chunk<F>::WBUF;
 
     // two chunks in flight per wave; the first two are fetched before the
     // activations are staged
     XStage<Fmt<F>, WG1> xs;
-    stage_load<Fmt<F>, WG1>(xs, a.x, a.U, 0);  // activation loads before weight loads
+    stage_load<Fmt<F>, WG1>(xs, a.x, NT * a.U, 0, a.U, a.K);  // activation loads first
     Pos ld{first, 0}, cp{first, 0};
     Fetch<F> f0, f1;
     fetch<F>(f0, a, ld, lane);
     ld.next(nc, stride);
     fetch<F>(f1, a, ld, lane);
     ld.next(nc, stride);
-    stage_build<Fmt<F>, WG1>(lds, xs, a.x, a.U, 0);
+    stage_build<Fmt<F>, WG1>(lds, xs, a.x, NT * a.U, 0, a.U, a.K);
 
-    float acc = 0.0f;
+    float acc[NT];
+#pragma unroll
+    for (int m = 0; m < NT; ++m) acc[m] = 0.0f;
     while (cp.row < a.N) {
         // a block of up to 64 rows with an even number of chunks
         const int rows_left = (a.N - 1 - cp.row) / stride + 1;
@@ -189,19 +201,24 @@ __global__ __launch_bounds__(WG1) void gemv1_kernel(GemvArgs a) {
         if ((nrows * nc) & 1) nrows -= nrows > 1 ? 1 : 0;
         const int nchunks = nrows * nc;
         const int row0 = cp.row;
-        float res = 0.0f;
+        float res[NT];
+#pragma unroll
+        for (int m = 0; m < NT; ++m) res[m] = 0.0f;
         int k = 0;
         for (int i = 0; i + 1 < nchunks; i += 2) {
-            step<F, BIAS>(f0, ld, cp, a, wbuf, lds, lane, nc, stride, acc, res, k);
-            step<F, BIAS>(f1, ld, cp, a, wbuf, lds, lane, nc, stride, acc, res, k);
+            step<F, BIAS, NT>(f0, ld, cp, a, wbuf, lds, lane, nc, stride, acc, res, k);
+            step<F, BIAS, NT>(f1, ld, cp, a, wbuf, lds, lane, nc, stride, acc, res, k);
         }
         if (nchunks & 1) {  // only the wave's very last row can end here
-            step<F, BIAS>(f0, ld, cp, a, wbuf, lds, lane, nc, stride, acc, res, k);
+            step<F, BIAS, NT>(f0, ld, cp, a, wbuf, lds, lane, nc, stride, acc, res, k);
             Fetch<F> t = f0;
             f0 = f1;
             f1 = t;
         }
-        if (lane < k) a.y[row0 + lane * stride] = res;
+        if (lane < k) {
+#pragma unroll
+            for (int m = 0; m < NT; ++m) a.y[(size_t)m * a.N + row0 + lane * stride] = res[m];
+        }
     }
 }
 
@@ -336,8 +353,25 @@ const void* gemv1_kernel_fn(int dtype, bool bias, int wg) {
 }
 
 template <int F>
-static size_t lds_of(int U, int wg) {
-    return (size_t)U * RECB + (size_t)(wg / 64) * Chunk<F>::WBUF;
+static size_t lds_of(int U, int wg, int nt = 1) {
+    return (size_t)nt * U * RECB + (size_t)(wg / 64) * Chunk<F>::WBUF;
+}
+
+// Several tokens (2 <= nt <= 4) at 1024 threads.
+const void* gemv1_multi_fn(int dtype, bool bias, int nt, size_t* lds, int U) {
+    return with_format(dtype, (const void*)nullptr, [&](auto f) -> const void* {
+        constexpr int F = decltype(f)::value;
+        *lds = lds_of<F>(U, 1024, nt);
+        switch (nt) {
+            case 2: return bias ? (const void*)&gemv1_kernel<F, true, 1024, 2>
+                                : (const void*)&gemv1_kernel<F, false, 1024, 2>;
+            case 3: return bias ? (const void*)&gemv1_kernel<F, true, 1024, 3>
+                                : (const void*)&gemv1_kernel<F, false, 1024, 3>;
+            case 4: return bias ? (const void*)&gemv1_kernel<F, true, 1024, 4>
+                                : (const void*)&gemv1_kernel<F, false, 1024, 4>;
+            default: return nullptr;
+        }
+    });
 }
 
 size_t gemv1_lds_bytes(int dtype, int U, int wg) {

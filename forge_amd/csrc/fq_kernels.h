@@ -26,6 +26,8 @@ struct GemvArgs {
 // batch-1 persistent kernel (fq_gemv1.hip)
 const void* gemv1_kernel_fn(int dtype, bool bias, int wg);
 size_t gemv1_lds_bytes(int dtype, int U, int wg);
+// batch-1 chunk kernel over 2..4 tokens sharing each weight fetch (a.M tokens)
+const void* gemv1_multi_fn(int dtype, bool bias, int nt, size_t* lds, int U);
 hipError_t launch_gemv1(int dtype, const GemvArgs& a, int grid, int wg, hipStream_t st);
 const void* gemv1r_kernel_fn(int dtype, int U, int row_bytes, bool bias, int* npr_out,
                              size_t* lds_out, int* wg_out);

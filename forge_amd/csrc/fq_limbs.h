@@ -37,10 +37,16 @@ __device__ __forceinline__ float wave_sum(float v) {
 constexpr int RECB = 144;
 constexpr int XPMAX = 10;  // activation loads a thread keeps in flight
 
+// Task t = 8 w + i: slots 4i .. 4i+3 of record w.  With U > 0 the records
+// of several tokens follow each other (U records, K activations per token);
+// U = 0: one token.  w0 offsets the record index within a token.
 template <class Fm>
-__device__ __forceinline__ float4 stage_x4(const float* __restrict__ x, int w0, int t) {
+__device__ __forceinline__ float4 stage_x4(const float* __restrict__ x, int w0, int t, int U,
+                                           int K) {
     const int w = t >> 3, i = t & 7;
-    return *reinterpret_cast<const float4*>(x + Fm::k_of(w0 + w, 4 * i));
+    int m = 0;
+    if (U > 0) m = w / U;  // uniform branch: no division for one token
+    return *reinterpret_cast<const float4*>(x + (size_t)m * K + Fm::k_of(w0 + w - m * U, 4 * i));
 }
 
 template <class Fm, int WG>
@@ -48,14 +54,15 @@ struct XStage {
     float4 v[XPMAX];
 };
 
+// nrec records in all; U records per token (0: one token).
 template <class Fm, int WG>
 __device__ __forceinline__ void stage_load(XStage<Fm, WG>& st, const float* __restrict__ x,
-                                           int nrec, int w0) {
+                                           int nrec, int w0, int U = 0, int K = 0) {
     const int tasks = 8 * nrec;
 #pragma unroll
     for (int p = 0; p < XPMAX; ++p)
         if (p * WG < tasks)  // uniform
-            st.v[p] = stage_x4<Fm>(x, w0, min(p * WG + (int)threadIdx.x, tasks - 1));
+            st.v[p] = stage_x4<Fm>(x, w0, min(p * WG + (int)threadIdx.x, tasks - 1), U, K);
 }
 
 template <int CTRL>
@@ -124,7 +131,8 @@ __device__ __forceinline__ void build_task(uint8_t* lds, float4 xv, int t, int t
 
 template <class Fm, int WG, bool SYNC = true>
 __device__ __forceinline__ void stage_build(uint8_t* lds, const XStage<Fm, WG>& st,
-                                            const float* __restrict__ x, int nrec, int w0) {
+                                            const float* __restrict__ x, int nrec, int w0,
+                                            int U = 0, int K = 0) {
     const int tasks = 8 * nrec;
 #pragma unroll
     for (int p = 0; p < XPMAX; ++p) {
@@ -133,7 +141,7 @@ __device__ __forceinline__ void stage_build(uint8_t* lds, const XStage<Fm, WG>& 
     // rows longer than XPMAX * WG / 8 records: the rest, loaded and built in turn
     for (int base = XPMAX * WG; base < tasks; base += WG) {
         const int t = base + (int)threadIdx.x;
-        build_task<Fm>(lds, stage_x4<Fm>(x, w0, min(t, tasks - 1)), t, tasks);
+        build_task<Fm>(lds, stage_x4<Fm>(x, w0, min(t, tasks - 1), U, K), t, tasks);
     }
     if (SYNC) __syncthreads();
 }
