@@ -112,7 +112,7 @@ int run_mmq(uint32_t dtype, const Geometry& g, const float* x, const void* w, co
     fq::mmq_shape(shape, &bn, &bm);
     const int gx = (N + bn - 1) / bn, gy = (Tp + bm / 16 - 1) / (bm / 16);
     const long tiles = (long)gx * gy;
-    int splits = (int)std::max(1L, std::min<long>((2L * di.cus + tiles - 1) / tiles, 8));
+    int splits = (int)std::max(1L, std::min<long>((4L * di.cus + tiles - 1) / tiles, 8));
     splits = std::max(1, std::min(splits, NC / 4));
     const size_t xop_b = (size_t)Tp * NC * 2048 * 2, xsum_b = (size_t)Tp * NC * 64 * 4,
                  ex_b = (size_t)Tp * NC * 16 * 4;
@@ -209,6 +209,50 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
                 return e == hipSuccess ? FQ_OK : hip_fail(e);
             }
         }
+    }
+
+    if (fq::mmqi_supported((int)dtype) && M >= 3 && M <= 8 && K > 0) {
+        // Q4_K, 3..8 tokens: the int8 matrix-core kernel in one pass (M = 2 is
+        // faster on the multi-token batch-1 kernel, M > 8 on the fp16 MFMA path)
+        const long T = (N + 15) / 16;
+        const long G = std::max(1L, std::min<long>(di.cus, T));
+        const int tpw = (int)((T + G - 1) / G);
+        bool ok = true;
+        for (int m0 = 0; m0 < M && ok; m0 += 8) {
+            const int mt = std::min(8, M - m0);
+            size_t lds = 0;
+            int wg = 0;
+            // chunk: >= 3 steps, about 4 per wave
+            int chunk = 3;
+            const void* fn = nullptr;
+            for (int pass = 0; pass < 2; ++pass) {
+                const int waves = (pass == 0 && mt <= 4) ? 16 : 8;
+                chunk = (int)std::max(3L, std::min(16L, (long)tpw * (K / 256) / (4L * waves)));
+                fn = fq::mmqi_kernel_fn(mt, bias_mode != 0, K, tpw, chunk,
+                                        std::min<size_t>(di.lds, 160 * 1024), &lds, &wg);
+                if (fn && wg / 64 == waves) break;
+            }
+            if (!fn) {
+                ok = false;
+                break;
+            }
+            fq::GemvArgs a{};
+            a.x = x + (size_t)m0 * K;
+            a.w = static_cast<const uint8_t*>(w);
+            a.y = y + (size_t)m0 * N;
+            a.bias = bias_mode == 2 ? bias + (size_t)m0 * N : bias;
+            a.bias_len = bias_mode == 0 ? 0 : bias_len;
+            a.bias_mode = bias_mode;
+            a.M = mt;
+            a.K = K;
+            a.N = N;
+            a.U = (int)T;
+            a.Uc = chunk;
+            a.row_bytes = (K / g.be) * g.bb;
+            e = fq::launch_raw(fn, a, (int)G, wg, lds, st);
+            if (e != hipSuccess) return hip_fail(e);
+        }
+        if (ok) return FQ_OK;
     }
 
     if (M >= 2 && M <= 4 && K > 0) {

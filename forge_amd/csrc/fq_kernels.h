@@ -45,6 +45,11 @@ hipError_t launch_silu_mul(const float* gate, const float* up, float* y, size_t 
 // y[m][off + n] = src[m][n] for n < n_src (rows of y are ld floats long)
 hipError_t launch_copy_cols(const float* src, float* y, int M, int n_src, int ld, int off, int cus,
                             hipStream_t st);
+// 2..8 tokens per pass, Q4_K on the int8 matrix cores (fq_mmqi.hip): a.M tokens,
+// a.U tiles of 16 rows, a.Uc steps per chunk
+bool mmqi_supported(int dtype);
+const void* mmqi_kernel_fn(int mt_needed, bool bias, int K, int tiles_per_wg, int chunk,
+                           size_t lds_cap, size_t* lds, int* wg);
 // M > 1 on MFMA (fq_mmq.hip)
 struct MmqArgs {
     const uint8_t* w;     // GGUF rows

@@ -10,6 +10,16 @@
 
 namespace fq {
 
+// Work-group barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every global load in flight (its release fence covers global
+// memory), which would stall a kernel that issues weight loads before the
+// barrier until they have all arrived.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Full 64-lane sum; the result is valid in lane 63.
 __device__ __forceinline__ float wave_sum(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, false));
@@ -91,10 +101,17 @@ __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
            (((uint32_t)(int)c & 0xFFu) << 16) | ((uint32_t)(int)d << 24);
 }
 
-template <class Fm>
-__device__ __forceinline__ void build_task(uint8_t* lds, float4 xv, int t, int tasks) {
-    constexpr int NG = Fm::NG, GS = 32 / NG;
-    const int i = t & 7;
+// The limbs of four consecutive activations (one float4) of a 32-slot unit
+// whose eight aligned lanes work together: a1, a2, a3 packed four to a dword,
+// the unit's power-of-two scale s1, and the sum of the activations over
+// aligned groups of GS slots (GS / 4 lanes).
+struct LimbQuad {
+    uint32_t a1, a2, a3;
+    float s1, gs;
+};
+
+template <int GS>
+__device__ __forceinline__ LimbQuad limb_quad(float4 xv) {
     float m = fmaxf(fmaxf(__builtin_fabsf(xv.x), __builtin_fabsf(xv.y)),
                     fmaxf(__builtin_fabsf(xv.z), __builtin_fabsf(xv.w)));
     m = group_max8(m);
@@ -119,13 +136,22 @@ __device__ __forceinline__ void build_task(uint8_t* lds, float4 xv, int t, int t
     if (!(m <= 3.0e38f)) s1 = __builtin_nanf("");  // Inf/NaN in x propagates
     float gs = (xv.x + xv.y) + (xv.z + xv.w);
     if (GS >= 8) gs = group_sum<GS / 4>(gs);
+    return LimbQuad{pack4(a1[0], a1[1], a1[2], a1[3]), pack4(a2[0], a2[1], a2[2], a2[3]),
+                    pack4(a3[0], a3[1], a3[2], a3[3]), s1, gs};
+}
+
+template <class Fm>
+__device__ __forceinline__ void build_task(uint8_t* lds, float4 xv, int t, int tasks) {
+    constexpr int NG = Fm::NG, GS = 32 / NG;
+    const int i = t & 7;
+    const LimbQuad lq = limb_quad<GS>(xv);
     if (t < tasks) {
         uint8_t* rec = lds + RECB * (t >> 3);
-        reinterpret_cast<uint32_t*>(rec)[i] = pack4(a1[0], a1[1], a1[2], a1[3]);
-        reinterpret_cast<uint32_t*>(rec + 32)[i] = pack4(a2[0], a2[1], a2[2], a2[3]);
-        reinterpret_cast<uint32_t*>(rec + 64)[i] = pack4(a3[0], a3[1], a3[2], a3[3]);
-        if (i == 0) *reinterpret_cast<float*>(rec + 96) = s1;
-        if ((4 * i) % GS == 0) reinterpret_cast<float*>(rec + 100)[(4 * i) / GS] = gs;
+        reinterpret_cast<uint32_t*>(rec)[i] = lq.a1;
+        reinterpret_cast<uint32_t*>(rec + 32)[i] = lq.a2;
+        reinterpret_cast<uint32_t*>(rec + 64)[i] = lq.a3;
+        if (i == 0) *reinterpret_cast<float*>(rec + 96) = lq.s1;
+        if ((4 * i) % GS == 0) reinterpret_cast<float*>(rec + 100)[(4 * i) / GS] = lq.gs;
     }
 }
 

@@ -95,3 +95,14 @@ def test_bias_and_determinism(dtype):
     np.testing.assert_allclose(y2, y0 + b2, rtol=0, atol=tol)
     y0b = run(dtype, w, x, N, K)
     assert np.array_equal(y0.view(np.uint32), y0b.view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [3, 5, 8])
+@pytest.mark.parametrize("N,K", [(1, 256), (17, 4096), (333, 1024), (200, 12800), (40, 18944)])
+def test_q4k_small_batch_int8_path(M, N, K):
+    # Q4_K, 3 <= M <= 8: the int8 matrix-core kernel (fq_mmqi.hip) where its
+    # activation staging fits in LDS, the fp16 MFMA path otherwise (K = 18944)
+    x = synth.make_x(M, K, seed=N + M)
+    y = check(F.Q4_K, N, K, x, seed=K + M, what=f"q4_k M={M} {N}x{K}")
+    y2 = check(F.Q4_K, N, K, x, seed=K + M, what="again")
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))  # deterministic
