@@ -50,8 +50,8 @@ def alg_bytes(dtype, N, K, M=1):
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=300)
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--configs", action="store_true", help="also time configs 0-4 (stderr)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)

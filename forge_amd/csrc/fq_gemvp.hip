@@ -201,14 +201,17 @@ struct Claims {
 };
 
 // Uniform claim of the next item from the work-group's LDS counter.
-__device__ __forceinline__ It claim(const Claims& cl, int lane) {
-    int i = 0;
-    if (lane == 0) i = atomicAdd(cl.ctr, 1);
-    i = __builtin_amdgcn_readfirstlane(i);
+__device__ __forceinline__ It item(const Claims& cl, int i) {
     const int f0 = i * CR;
     if (f0 >= cl.total) return It{0, 0, 0, 0, 0};
     const int s = f0 / cl.rows;
     return It{f0, min(CR, cl.total - f0), 0, s, f0 - s * cl.rows};
+}
+
+__device__ __forceinline__ It claim(const Claims& cl, int lane) {
+    int i = 0;
+    if (lane == 0) i = atomicAdd(cl.ctr, 1);
+    return item(cl, __builtin_amdgcn_readfirstlane(i));
 }
 
 // The item the load side has claimed beyond the compute side's item (n = 0:
@@ -337,18 +340,26 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
 
     // limb records first, so the activation loads never queue behind the
     // weight stream; then the first D steps of weight loads
-    if (threadIdx.x == 0) ctr = 0;
+    // item w is wave w's first (the counter hands out the rest); its first
+    // step's weight loads go out between the activation loads and the limb
+    // build, so HBM is busy during the staging without delaying the
+    // activations (the remaining first loads follow the barrier: issued all
+    // at once they would queue ahead of other work-groups' activation loads)
+    constexpr int W = WG / 64;
+    if (threadIdx.x == 0) ctr = W;
+    It q{0, 0, 0, 0, 0};
+    It ld = item(cl, __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6)), cp = ld;
+    typename P::Raw f[D][NL];
     {
         XStage<P, WG> xs;
         stage_load<P, WG>(xs, a.x, a.Uc, 0);
+        pload<F, NL, MODE>(f[0], a, ld, lo, lane);
         stage_build<P, WG, false>(lds, xs, a.x, a.Uc, 0);
     }
-    __syncthreads();
-    It q{0, 0, 0, 0, 0};
-    It ld = claim(cl, lane), cp = ld;
-    typename P::Raw f[D][NL];
+    lds_barrier();  // the weight loads stay in flight
+    advance_load(ld, q, cl, lane);
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
+    for (int j = 1; j < D; ++j) {
         pload<F, NL, MODE>(f[j], a, ld, lo, lane);
         advance_load(ld, q, cl, lane);
     }
