@@ -1,0 +1,108 @@
+"""GPU parity of the prefill path (M > 32, fq_mmq.hip) against the oracle.
+
+Edge cases beyond the token-count and format sweeps of test_gpu_mmq.py, for
+the two prefill formats of the benchmark (Q8_0, Q4_0): N and M tails with
+one row and one block of K, block scales up to the fp16 maximum (and fp16
+subnormal ones in the same row), activations spanning 60 decades inside one
+token, bias modes, determinism, and an activation pointer that is only
+4-byte aligned.  Bars as in test_gpu_parity.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from forge_amd import formats as F
+from forge_amd import ops, synth
+from helpers import assert_close
+from test_gpu_parity import dev_weight, run
+
+pytestmark = pytest.mark.gpu
+
+PREFILL = [F.Q8_0, F.Q4_0]
+
+
+def check(dtype, w, x, N, K, what, bias=None):
+    y = run(dtype, w, x, N, K, bias=bias)
+    y64 = oracle.matmul_f64(dtype, x, w, N, K)
+    if bias is not None:
+        y64 = y64 + bias.cpu().numpy().astype(np.float64)
+    deq_max = float(np.max(np.abs(oracle.dequant(dtype, w, N, K))))
+    assert_close(y, y64, x, np.array([deq_max]), what)
+    return y
+
+
+@pytest.mark.parametrize("dtype", PREFILL)
+@pytest.mark.parametrize("M,N,K", [(33, 1, 32), (40, 129, 4096), (64, 1024, 2048),
+                                   (100, 333, 1024), (200, 2048, 512), (65, 16, 18944)])
+def test_shapes(dtype, M, N, K):
+    w = synth.make_weights(dtype, N, K, seed=M + N)
+    x = synth.make_x(M, K, seed=K + M)
+    check(dtype, w, x, N, K, f"{F.fmt(dtype).name} M={M} {N}x{K}")
+
+
+@pytest.mark.parametrize("dtype", PREFILL)
+def test_large_block_scales(dtype):
+    # block scales up to the fp16 maximum in some rows (|q d| far outside the
+    # fp16 range); one row mixes the largest scale with fp16 subnormal ones
+    M, N, K = 48, 256, 2048
+    f = F.fmt(dtype)
+    w = synth.make_weights(dtype, N, K, seed=21).reshape(N, K // 32, f.block_bytes)
+    rng = np.random.default_rng(22)
+    big = np.array([300.0, 4000.0, 65504.0, -20000.0], np.float16)
+    for r in (0, 5, 130, 255):
+        cols = rng.choice(K // 32, size=8, replace=False)
+        w[r, cols, 0:2] = rng.choice(big, size=8).view(np.uint8).reshape(8, 2)
+    w[77, :, 0:2] = np.array([1e-7], np.float16).view(np.uint8)  # subnormal
+    w[77, 3, 0:2] = np.array([65504.0], np.float16).view(np.uint8)
+    w[200, :, 0:2] = np.array([1000.0], np.float16).view(np.uint8)  # a whole row
+    w = w.reshape(N, -1)
+    x = synth.make_x(M, K, seed=23)
+    check(dtype, w, x, N, K, f"{F.fmt(dtype).name} large scales")
+
+
+@pytest.mark.parametrize("dtype", PREFILL)
+def test_activation_magnitudes(dtype):
+    # 64-element stretches from 1e-30 to 1e30, a zero stretch and an all-zero
+    # token
+    M, K = 40, 1024
+    x = synth.make_x(M, K, seed=5)
+    scales = 10.0 ** np.linspace(-30, 30, K // 64)
+    x = (x.reshape(M, K // 64, 64) * scales[None, :, None].astype(np.float32)).reshape(M, K)
+    x[3, 128:192] = 0.0
+    x[7] = 0.0
+    x = x.astype(np.float32)
+    w = synth.make_weights(dtype, 96, K, seed=11)
+    y = check(dtype, w, x, 96, K, f"{F.fmt(dtype).name} magnitudes")
+    assert np.all(y[7] == 0.0)
+
+
+@pytest.mark.parametrize("dtype", PREFILL)
+def test_bias_and_determinism(dtype):
+    M, N, K = 100, 300, 1024
+    w = synth.make_weights(dtype, N, K, seed=3)
+    x = synth.make_x(M, K, seed=4)
+    b1 = torch.from_numpy(synth.make_x(1, N, seed=5).reshape(N)).cuda()
+    b2 = torch.from_numpy(synth.make_x(M, N, seed=6)).cuda()
+    y0 = check(dtype, w, x, N, K, "no bias")
+    check(dtype, w, x, N, K, "row bias", bias=b1)
+    check(dtype, w, x, N, K, "full bias", bias=b2)
+    y0b = run(dtype, w, x, N, K)
+    assert np.array_equal(y0.view(np.uint32), y0b.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", PREFILL)
+def test_unaligned_activations(dtype):
+    # x at a 4-byte offset from a 16-byte aligned allocation
+    M, N, K = 50, 200, 512
+    w_np = synth.make_weights(dtype, N, K, seed=8)
+    x_np = synth.make_x(M, K, seed=9)
+    buf = torch.empty(M * K + 1, dtype=torch.float32, device="cuda")
+    buf[1:] = torch.from_numpy(x_np.reshape(-1)).cuda()
+    x = buf[1:].view(M, K)
+    y = ops.matmul_transB(x, dev_weight(dtype, w_np, N, K, 0)).cpu().numpy()
+    y64 = oracle.matmul_f64(dtype, x_np, w_np, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(dtype, w_np, N, K))))
+    assert_close(y, y64, x_np, np.array([deq_max]), "unaligned x")
