@@ -175,7 +175,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this hot path is single-GPU by design "
-              "(row-sharding across GPUs is described in DESIGN.md, not implemented); "
+              "(sharding the rows across GPUs is a design, not implemented); "
               "run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
