@@ -17,7 +17,9 @@ served from the 256 MB Infinity Cache.  Prints ONE JSON line:
   cpu_baseline  the reference's own AVX2+OpenMP ops::matmul_transB (compiled
              from its sources into oracle/_ref) on the same step, on this
              host's cores.
---configs additionally prints per-config lines (configs 0-4) to stderr.
+--configs additionally prints per-config lines (configs 0-4) to stderr, each
+with the reference CPU path timed on a row sample of the same weights
+(skipped with --no-cpu).
 """
 from __future__ import annotations
 
@@ -109,7 +111,39 @@ def cpu_baseline(host_w, host_x, budget_s):
     }
 
 
-def time_config(name, dtype, N, K, M, reps=20, pool_bytes=600 << 20, packed=False):
+def cpu_config(dtype, w_np, N, K, M, budget_s=1.0):
+    """The reference CPU path (oracle/_ref, AVX2 + OpenMP) on a bounded row
+    sample of one config: the first rows of the same weights, median over
+    ~budget_s, scaled to all N rows (the reference parallelises over rows)."""
+    import oracle
+    from forge_amd import synth
+    if not oracle.have_ref():
+        return None
+    threads = cpu_threads()
+    L = oracle.load_ref()
+    x = np.ascontiguousarray(synth.make_x(M, K, 1))
+    # about 2^27 multiply-adds per call, at least 64 rows (all when fewer)
+    rows = max(min(N, 64), min(N, (1 << 27) // max(1, M * K)))
+    w = np.ascontiguousarray(w_np[:rows])
+    y = np.empty((M, rows), np.float32)
+
+    def call():
+        if L.fqr_matmul_transB(dtype, oracle._p(x), oracle._p(w), oracle._p(y), M, K, rows,
+                               threads) != 0:
+            raise RuntimeError("reference matmul_transB failed")
+
+    call()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    us = statistics.median(times) * 1e6 * N / rows
+    return {"cpu_ref_us": round(us, 1), "cpu_rows": rows, "cpu_threads": threads}
+
+
+def time_config(name, dtype, N, K, M, reps=20, pool_bytes=600 << 20, packed=False, cpu=False):
     """Average per-call device time of one matmul shape.  `reps` calls over
     rotated weight copies (>= 600 MB, so calls stream from HBM) are captured
     in one HIP graph, so host launch cost does not hide small kernels; the
@@ -166,6 +200,11 @@ def time_config(name, dtype, N, K, M, reps=20, pool_bytes=600 << 20, packed=Fals
         tf = 2.0 * M * N * K / us / 1e6
         line["TFLOPs"] = round(tf, 1)
         line["pct_fp16_mfma"] = round(100 * tf / PEAK_FP16_TFLOPS, 2)
+    if cpu and not packed:
+        c = cpu_config(dtype, w_np, N, K, M)
+        if c:
+            line.update(c)
+            line["gpu_speedup"] = round(c["cpu_ref_us"] / us, 1)
     del g, ws, base
     torch.cuda.empty_cache()
     return line
@@ -322,7 +361,7 @@ def main():
     print(json.dumps(out), flush=True)
 
     if args.configs:
-        for line in all_configs():
+        for line in all_configs(cpu=not args.no_cpu):
             print(json.dumps(line), file=sys.stderr, flush=True)
 
 
@@ -395,32 +434,32 @@ def time_fused(name, dtype, N, K, reps=20, pool_bytes=600 << 20):
     return out
 
 
-def all_configs():
+def all_configs(cpu=False):
     Q4_0, Q8_0, Q4_K, Q6_K = 2, 7, 4, 13
     lines = []
     for pk in (False, True):
-        lines.append(time_config("cfg0", Q4_0, 5632, 2048, 1, packed=pk))
+        lines.append(time_config("cfg0", Q4_0, 5632, 2048, 1, packed=pk, cpu=cpu))
         for dt in (Q4_0, Q8_0):
             for n, N, K in [("q", 2048, 2048), ("k", 256, 2048), ("o", 2048, 2048),
                             ("gate", 5632, 2048), ("down", 2048, 5632)]:
                 lines.append(time_config(f"cfg1-{n}-{'q4_0' if dt == Q4_0 else 'q8_0'}", dt, N,
-                                         K, 1, packed=pk))
+                                         K, 1, packed=pk, cpu=cpu))
         for n, dt, N, K in [("gate", Q4_K, 18944, 3584), ("down", Q6_K, 3584, 18944),
                             ("lm_head", Q6_K, 152064, 3584)]:
-            lines.append(time_config(f"cfg2-{n}", dt, N, K, 1, packed=pk))
+            lines.append(time_config(f"cfg2-{n}", dt, N, K, 1, packed=pk, cpu=cpu))
     lines.append(time_fused("cfg2-gate+up", Q4_K, 18944, 3584))
     lines.append(time_fused("cfg1-gate+up-q4_0", Q4_0, 5632, 2048))
     lines.append(time_config("cfg3", Q4_K, 14336, 4096, 1, packed=True))
     for M in (1, 2, 4, 8, 16):
-        lines.append(time_config("cfg3", Q4_K, 14336, 4096, M))
+        lines.append(time_config("cfg3", Q4_K, 14336, 4096, M, cpu=cpu))
     for dt in (Q8_0, Q4_0):
         for N in (4096, 14336):
             lines.append(time_config(f"cfg4-{'q8_0' if dt == Q8_0 else 'q4_0'}", dt, N, 4096, 512,
-                                     reps=10))
+                                     reps=10, cpu=cpu))
     # the formats outside the benchmark configs, at the 7B gate shape (GGUF layout)
     for name, dt in (("q5_0", 8), ("q5_1", 9), ("q3_k", 11), ("q5_k", 12), ("iq4_nl", 17)):
         for M in (1, 8):
-            lines.append(time_config(f"fmt-{name}", dt, 18944, 3584, M))
+            lines.append(time_config(f"fmt-{name}", dt, 18944, 3584, M, cpu=cpu))
     return lines
 
 
