@@ -170,17 +170,19 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         return e == hipSuccess ? FQ_OK : hip_fail(e);
     }
 
-    if (M == 1 && K > 0) {
-        // batch 1: persistent work-groups, as many as fit on every CU
+    if ((M == 1 || M == 2) && K > 0) {
+        // batch 1 (and two tokens on rows of at most 128 units, where the
+        // row-step kernel keeps both tokens' limbs in registers): persistent
+        // work-groups, as many as fit on every CU
         const int U1 = K / 32;
         int wg = 1024;
-        size_t lds = fq::gemv1_lds_bytes((int)dtype, U1, wg);
-        const void* fn = fq::gemv1_kernel_fn((int)dtype, bias_mode != 0, wg);
+        size_t lds = M == 1 ? fq::gemv1_lds_bytes((int)dtype, U1, wg) : 0;
+        const void* fn = M == 1 ? fq::gemv1_kernel_fn((int)dtype, bias_mode != 0, wg) : nullptr;
         int npr = 0;
         size_t lds_r = 0;
         int wg_r = 0;
         const void* fr = fq::gemv1r_kernel_fn((int)dtype, U1, (K / g.be) * g.bb, bias_mode != 0,
-                                              &npr, &lds_r, &wg_r);
+                                              &npr, &lds_r, &wg_r, M);
         if (fr && lds_r <= std::min<size_t>(di.lds, 160 * 1024)) {
             fn = fr;
             lds = lds_r;
@@ -198,7 +200,7 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
                 a.bias = bias;
                 a.bias_len = bias_mode == 0 ? 0 : bias_len;
                 a.bias_mode = bias_mode;
-                a.M = 1;
+                a.M = M;
                 a.K = K;
                 a.N = N;
                 a.U = U1;

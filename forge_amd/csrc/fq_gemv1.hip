@@ -251,66 +251,88 @@ __device__ __forceinline__ void rspill(const RowFetch<NPR>& f, uint8_t* wbuf, in
     for (int i = 0; i < NPR; ++i) reinterpret_cast<uint4*>(wbuf)[lane + 64 * i] = f.v[i];
 }
 
-template <int F, int NC, int NPR, bool BIAS>
+// NT tokens: each unit is loaded and unpacked once and dotted with every
+// token's limbs (L[m * NC + c]); bias_mode 2 adds bias[m N + row].
+template <int F, int NC, int NPR, bool BIAS, int NT>
 __device__ __forceinline__ void row_step(RowFetch<NPR>& f, int row, int prefetch_row,
                                          const GemvArgs& a, uint8_t* wbuf, const Limbs* L,
-                                         int lane, float& res, int& k) {
+                                         int lane, float (&res)[NT], int& k) {
     __builtin_amdgcn_sched_barrier(0);
     rspill<NPR>(f, wbuf, lane);
     rfetch<NPR>(f, a, prefetch_row, lane);
     const uint8_t* g0 = a.w + (size_t)min(row, a.N - 1) * a.row_bytes;
     const uint8_t* rowp = wbuf + (reinterpret_cast<uintptr_t>(g0) & 15);
-    float acc = 0.0f;
+    float acc[NT];
+#pragma unroll
+    for (int m = 0; m < NT; ++m) acc[m] = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int u = lane + 64 * c;
         const int ul = min(u, a.U - 1);
-        const float t = limb_dot<F>(Fmt<F>::template load<false>(rowp, ul), ul, L[c]);
-        acc += u < a.U ? t : 0.0f;
+        const auto raw = Fmt<F>::template load<false>(rowp, ul);
+#pragma unroll
+        for (int m = 0; m < NT; ++m) {
+            const float t = limb_dot<F>(raw, ul, L[m * NC + c]);
+            acc[m] += u < a.U ? t : 0.0f;
+        }
     }
-    float s = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
-    if constexpr (BIAS) {
-        const int r = min(row, a.N - 1);
-        s += r < a.bias_len ? ((const_fp)(uintptr_t)a.bias)[r] : 0.0f;
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+        float s = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc[m])), 63));
+        if constexpr (BIAS) {
+            const int r = min(row, a.N - 1);
+            if (a.bias_mode == 2)
+                s += ((const_fp)(uintptr_t)a.bias)[(size_t)m * a.N + r];
+            else
+                s += r < a.bias_len ? ((const_fp)(uintptr_t)a.bias)[r] : 0.0f;
+        }
+        res[m] = lane == k ? s : res[m];
     }
-    res = lane == k ? s : res;
     ++k;
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int F, int NC, int NPR, bool BIAS, int WG, int D>
+// NT tokens (a.M == NT): the records of all NT tokens are staged, and every
+// lane holds each token's limbs of its units in registers.
+template <int F, int NC, int NPR, bool BIAS, int WG, int D, int NT = 1>
 __global__ __launch_bounds__(WG) void gemv1r_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int stride = gridDim.x * (WG / 64);
     const int first = __builtin_amdgcn_readfirstlane(blockIdx.x * (WG / 64) + wave);
-    uint8_t* wbuf = lds + (size_t)a.U * RECB + wave * (NPR * 1024);
+    uint8_t* wbuf = lds + (size_t)NT * a.U * RECB + wave * (NPR * 1024);
 
     // D rows in flight per wave: buffer i always holds row (next + i * stride)
     XStage<Fmt<F>, WG> xs;
-    stage_load<Fmt<F>, WG>(xs, a.x, a.U, 0);  // activation loads before weight loads
+    // activation loads before weight loads
+    stage_load<Fmt<F>, WG>(xs, a.x, NT * a.U, 0, NT > 1 ? a.U : 0, a.K);
     RowFetch<NPR> f[D];
 #pragma unroll
     for (int i = 0; i < D; ++i) rfetch<NPR>(f[i], a, first + i * stride, lane);
-    stage_build<Fmt<F>, WG>(lds, xs, a.x, a.U, 0);
-    Limbs L[NC];
+    stage_build<Fmt<F>, WG>(lds, xs, a.x, NT * a.U, 0, NT > 1 ? a.U : 0, a.K);
+    Limbs L[NT * NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) read_limbs(L[c], lds, min(lane + 64 * c, a.U - 1));
+    for (int m = 0; m < NT; ++m)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            read_limbs(L[m * NC + c], lds, m * a.U + min(lane + 64 * c, a.U - 1));
 
     int row = first;
     while (row < a.N) {
         const int rows_left = (a.N - 1 - row) / stride + 1;
         const int nrows = rows_left < D ? rows_left : min(64, rows_left) / D * D;
         const int row0 = row;
-        float res = 0.0f;
+        float res[NT];
+#pragma unroll
+        for (int m = 0; m < NT; ++m) res[m] = 0.0f;
         int k = 0;
         if (nrows >= D) {
             for (int i = 0; i < nrows; i += D) {
 #pragma unroll
                 for (int j = 0; j < D; ++j) {
-                    row_step<F, NC, NPR, BIAS>(f[j], row, row + D * stride, a, wbuf, L, lane, res,
+                    row_step<F, NC, NPR, BIAS, NT>(f[j], row, row + D * stride, a, wbuf, L, lane, res,
                                                k);
                     row += stride;
                 }
@@ -319,13 +341,16 @@ __global__ __launch_bounds__(WG) void gemv1r_kernel(GemvArgs a) {
 #pragma unroll
             for (int j = 0; j < D - 1; ++j) {
                 if (j < nrows) {
-                    row_step<F, NC, NPR, BIAS>(f[j], row, row + D * stride, a, wbuf, L, lane, res,
+                    row_step<F, NC, NPR, BIAS, NT>(f[j], row, row + D * stride, a, wbuf, L, lane, res,
                                                k);
                     row += stride;
                 }
             }
         }
-        if (lane < k) a.y[row0 + lane * stride] = res;
+        if (lane < k) {
+#pragma unroll
+            for (int m = 0; m < NT; ++m) a.y[(size_t)m * a.N + row0 + lane * stride] = res[m];
+        }
     }
 }
 
@@ -384,44 +409,46 @@ constexpr int WGR = 512;
 #define FQ_ROW_DEPTH 3
 #endif
 
-template <int F, int NC, int NPR>
+template <int F, int NC, int NPR, int NT>
 static const void* rfn3(bool bias) {
     constexpr int D = FQ_ROW_DEPTH;
-    return bias ? reinterpret_cast<const void*>(&gemv1r_kernel<F, NC, NPR, true, WGR, D>)
-                : reinterpret_cast<const void*>(&gemv1r_kernel<F, NC, NPR, false, WGR, D>);
+    return bias ? reinterpret_cast<const void*>(&gemv1r_kernel<F, NC, NPR, true, WGR, D, NT>)
+                : reinterpret_cast<const void*>(&gemv1r_kernel<F, NC, NPR, false, WGR, D, NT>);
 }
 
-template <int F>
+template <int F, int NT>
 static const void* rfn(int nc, int npr, bool bias) {
     if (nc == 1) {
         switch (npr) {
-            case 1: return rfn3<F, 1, 1>(bias);
-            case 2: return rfn3<F, 1, 2>(bias);
-            case 3: return rfn3<F, 1, 3>(bias);
+            case 1: return rfn3<F, 1, 1, NT>(bias);
+            case 2: return rfn3<F, 1, 2, NT>(bias);
+            case 3: return rfn3<F, 1, 3, NT>(bias);
         }
     } else if (nc == 2) {
         switch (npr) {
-            case 2: return rfn3<F, 2, 2>(bias);
-            case 3: return rfn3<F, 2, 3>(bias);
-            case 4: return rfn3<F, 2, 4>(bias);
-            case 5: return rfn3<F, 2, 5>(bias);
+            case 2: return rfn3<F, 2, 2, NT>(bias);
+            case 3: return rfn3<F, 2, 3, NT>(bias);
+            case 4: return rfn3<F, 2, 4, NT>(bias);
+            case 5: return rfn3<F, 2, 5, NT>(bias);
         }
     }
     return nullptr;
 }
 
-// Row-step variant for U <= 128: returns nullptr when the shape does not fit.
+// Row-step variant for U <= 128 and nt = 1 or 2 tokens: returns nullptr when
+// the shape does not fit.
 const void* gemv1r_kernel_fn(int dtype, int U, int row_bytes, bool bias, int* npr_out,
-                             size_t* lds_out, int* wg_out) {
-    if (U > 128) return nullptr;
+                             size_t* lds_out, int* wg_out, int nt) {
+    if (U > 128 || nt < 1 || nt > 2) return nullptr;
     const int nc = U > 64 ? 2 : 1;
     const int npr = (row_bytes + 16 + 1023) / 1024;
     const void* fn = with_format(dtype, (const void*)nullptr, [&](auto f) {
-        return rfn<decltype(f)::value>(nc, npr, bias);
+        constexpr int F = decltype(f)::value;
+        return nt == 1 ? rfn<F, 1>(nc, npr, bias) : rfn<F, 2>(nc, npr, bias);
     });
     if (!fn) return nullptr;
     *npr_out = npr;
-    *lds_out = (size_t)U * RECB + (size_t)(WGR / 64) * npr * 1024;
+    *lds_out = (size_t)nt * U * RECB + (size_t)(WGR / 64) * npr * 1024;
     *wg_out = WGR;
     return fn;
 }

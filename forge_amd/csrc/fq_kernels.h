@@ -29,8 +29,9 @@ size_t gemv1_lds_bytes(int dtype, int U, int wg);
 // batch-1 chunk kernel over 2..4 tokens sharing each weight fetch (a.M tokens)
 const void* gemv1_multi_fn(int dtype, bool bias, int nt, size_t* lds, int U);
 hipError_t launch_gemv1(int dtype, const GemvArgs& a, int grid, int wg, hipStream_t st);
+// row-step kernel for rows of at most 128 units, over nt = 1 or 2 tokens (a.M)
 const void* gemv1r_kernel_fn(int dtype, int U, int row_bytes, bool bias, int* npr_out,
-                             size_t* lds_out, int* wg_out);
+                             size_t* lds_out, int* wg_out, int nt = 1);
 hipError_t launch_raw(const void* fn, const GemvArgs& a, int grid, int wg, size_t lds,
                       hipStream_t st);
 // packed-layout batch-1 kernels (fq_gemvp.hip)
