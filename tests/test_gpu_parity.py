@@ -199,8 +199,12 @@ def test_unaligned_weight_base(dtype):
     assert np.array_equal(y0, y2)
 
 
-def test_bias_modes():
-    dtype, N, K, M = F.Q4_K, 300, 1024, 3
+@pytest.mark.parametrize("dtype,M", [(F.Q4_K, 1), (F.Q4_K, 2), (F.Q4_K, 3), (F.Q6_K, 2),
+                                     (F.Q8_0, 2), (F.Q4_K, 40)])
+def test_bias_modes(dtype, M):
+    # every M path: batch 1, two tokens on the row-step kernel, the int8
+    # matrix cores (Q4_K, 3..8), the fp16 MFMA path
+    N, K = 300, 1024
     w = synth.make_weights(dtype, N, K, seed=11)
     x = synth.make_x(M, K, 12)
     base = run(dtype, w, x, N, K)
