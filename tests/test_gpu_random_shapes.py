@@ -1,0 +1,58 @@
+"""Seeded random shapes through ops.matmul_transB against the f64 oracle:
+every format, M from 1 to 100 (every dispatch path), N >= 16 with tails, K
+any whole number of blocks up to 8192, no bias / row bias / full bias.
+Bars as in test_gpu_parity.py.
+
+The rel-L2 bar is a ratio to |y|, so it is only asserted on outputs of 16
+or more rows: on a single row whose dot product cancels, |y| can be orders
+below ||x|| max|w| and the ratio exceeds 1e-5 for the reference's own fp32
+CPU path as well (see the numerics notes); the max-abs bar holds there."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from forge_amd import formats as F
+from forge_amd import ops, synth
+from helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+CASES = 160
+
+
+def _cases():
+    rng = np.random.default_rng(20260301)
+    out = []
+    allf = sorted(F.FORMATS)
+    while len(out) < CASES:
+        dt = int(rng.choice(allf))
+        be = F.fmt(dt).block_elems
+        M = int(rng.choice([1, 1, 2, 3, 4, 5, 8, 9, 16, 17, 31, 32, 33, 64, 100]))
+        N = int(rng.choice([16, 17, 100, 128, 129, 300, 1000]))
+        K = be * int(rng.integers(1, max(2, 8192 // be)))
+        if M * N * K > 1.5e8:
+            continue
+        out.append((dt, M, N, K, int(rng.integers(1 << 30)), float(rng.random())))
+    return out
+
+
+@pytest.mark.parametrize("dt,M,N,K,seed,r", _cases())
+def test_random_shape(dt, M, N, K, seed, r):
+    w = synth.make_weights(dt, N, K, seed=seed)
+    x = synth.make_x(M, K, seed=seed + 1)
+    bias = None
+    if r < 0.2:
+        bias = torch.from_numpy(synth.make_x(1, N, seed + 2).reshape(N))
+    elif r < 0.3:
+        bias = torch.from_numpy(synth.make_x(M, N, seed + 3))
+    W = ops.QWeight.from_numpy(w, dt, N, K, device="cuda")
+    y = ops.matmul_transB(torch.from_numpy(x).cuda(),
+                          W, bias.cuda() if bias is not None else None).cpu().numpy()
+    y64 = oracle.matmul_f64(dt, x, w, N, K)
+    if bias is not None:
+        y64 = y64 + bias.numpy().astype(np.float64)
+    deq = float(np.max(np.abs(oracle.dequant(dt, w, N, K))))
+    assert_close(y, y64, x, np.array([deq]), f"{F.fmt(dt).name} M={M} N={N} K={K}")
