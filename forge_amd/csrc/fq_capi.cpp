@@ -112,10 +112,13 @@ int run_mmq(uint32_t dtype, const Geometry& g, const float* x, const void* w, co
     fq::mmq_shape(shape, &bn, &bm);
     const int gx = (N + bn - 1) / bn, gy = (Tp + bm / 16 - 1) / (bm / 16);
     const long tiles = (long)gx * gy;
-    // K-splits only when the tiles alone leave CUs idle (measured on cfg4:
-    // 448 tiles run fastest unsplit, 128 tiles with 4 splits)
+    // K-splits only when the tiles alone leave CUs idle, to about two
+    // work-groups per CU for the 128x128 prefill tiles and three for the
+    // small-batch tiles (measured: cfg4 448 tiles fastest unsplit, 128 tiles
+    // with 4 splits; 18944-row Q5_K at M = 8 41 -> 37 us with 6 splits)
+    const long per_cu = shape == fq::MMQ_BIG ? 2 : 3;
     int splits = tiles >= di.cus ? 1
-                                 : (int)std::max(1L, std::min<long>((2L * di.cus + tiles - 1) / tiles, 8));
+                                 : (int)std::max(1L, std::min<long>((per_cu * di.cus + tiles - 1) / tiles, 8));
     splits = std::max(1, std::min(splits, NC / 4));
     const size_t xop_b = (size_t)Tp * NC * 2048 * 2, xsum_b = (size_t)Tp * NC * 64 * 4,
                  ex_b = (size_t)Tp * NC * 16 * 4;
