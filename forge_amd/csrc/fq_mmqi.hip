@@ -50,6 +50,15 @@ constexpr int DT = 3;  // steps in flight per wave
 // Partial-sum slots per tile: one per chunk that can overlap the tile.
 __host__ __device__ inline int slots(int S, int C) { return (S + C - 1) / C + 1; }
 
+// B staging: limb t of token m at positions 8 q .. 8 q + 7 of sub-block sbg.
+// A sub-block's 96 mt bytes are padded by 8: a wave's staging stores cover
+// eight sub-blocks at once, and an unpadded stride (768 B at mt = 8, a
+// multiple of the 256-byte bank row) put all eight on the same banks.
+__host__ __device__ constexpr int sbstride(int mt) { return 96 * mt + 8; }
+__device__ __forceinline__ int boff(int sbg, int t, int q, int m, int mt) {
+    return sbg * sbstride(mt) + ((t * 4 + q) * mt + m) * 8;
+}
+
 struct Layout {  // LDS byte offsets
     int s1, S, zero, wave, part, total;
     static constexpr int PANEL = 2304, WAVE = 2304 + 128 * 4;  // panel, wv
@@ -57,18 +66,13 @@ struct Layout {  // LDS byte offsets
 __host__ __device__ inline Layout layout(int K, int mt, int nw, int ntl, int C) {
     Layout L;
     const int NSB = K / 32;
-    L.s1 = NSB * 3 * 4 * mt * 8;
+    L.s1 = NSB * sbstride(mt);
     L.S = L.s1 + 4 * mt * NSB;
     L.zero = L.S + 4 * mt * NSB;
     L.wave = (L.zero + 16 + 15) & ~15;
     L.part = L.wave + nw * Layout::WAVE;
     L.total = L.part + ntl * slots(K / 256, C) * 16 * mt * 4;
     return L;
-}
-
-// B staging: limb t of token m at positions 8 q .. 8 q + 7 of sub-block sbg.
-__device__ __forceinline__ int boff(int sbg, int t, int q, int m, int mt) {
-    return (((sbg * 3 + t) * 4 + q) * mt + m) * 8;
 }
 
 // floor(i / S) for 0 <= i < 2^22 from a precomputed 1 / S (the quotient's
@@ -102,6 +106,9 @@ __device__ __forceinline__ void load_step(Raw& f, const GemvArgs& a, int S, floa
 template <int MT, int WG, bool BIAS>
 __global__ __launch_bounds__(WG) void mmqi_kernel(GemvArgs a) {
     constexpr int NWV = WG / 64;
+    // sub-block pairs unrolled: all four at 512 threads (up to 256 VGPRs),
+    // one at 1024 (128 VGPRs)
+    constexpr int JU = WG >= 1024 ? 1 : 4;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -119,14 +126,39 @@ __global__ __launch_bounds__(WG) void mmqi_kernel(GemvArgs a) {
     float* part = reinterpret_cast<float*>(lds + Lo.part);
 
     // ---- activations -> B staging (limbs), per-token sub-block scales and sums
+    // ---- work: chunks of C >= DT steps (see the head comment)
+    const int items = ntl * S;
+    const int nchunks = (items + C - 1) / C;
+    const int clampi = max(items - 1, 0);
+    int prow[3], pcol[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int p = min(lane + 64 * i, 143);
+        prow[i] = p / 9;
+        pcol[i] = p - 9 * prow[i];
+    }
+    int ld_pos = wave * C, ld_end = ld_pos < items ? min(items, ld_pos + C) : -1;
+    int cp_pos = ld_pos, cp_end = max(ld_end, ld_pos);
+    int pend_pos = -1, pend_end = -1, pend_k = 0;
+    int cp_k = wave;
+    Raw f[DT];
+
+    // ---- staging of every token's limbs, with the wave's first DT steps of
+    // weight loads (inside its first chunk: no claims yet) issued between the
+    // first activation loads and their limb build, so HBM streams while the
+    // work-group builds.  The activation loads are unconditional (tokens past
+    // M repeat the last one) so the compiler knows how many weight loads
+    // follow them.
     const int tpt = K / 4;  // tasks per token: 8 lanes per 32-element sub-block
-    for (int base = 0; base < tpt; base += WG) {
-        const int t = base + (int)threadIdx.x;
-        float4 v[MT];  // every token's loads in flight together
+    float4 v[MT];           // every token's loads in flight together
+    auto xload = [&](int base) {
+        const int t = min(base + (int)threadIdx.x, tpt - 1);
 #pragma unroll
         for (int m = 0; m < MT; ++m)
-            if (m < M)
-                v[m] = reinterpret_cast<const float4*>(a.x + (size_t)m * K)[min(t, tpt - 1)];
+            v[m] = reinterpret_cast<const float4*>(a.x + (size_t)min(m, M - 1) * K)[t];
+    };
+    auto xbuild = [&](int base) {
+        const int t = base + (int)threadIdx.x;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             if (m >= M) break;
@@ -144,34 +176,25 @@ __global__ __launch_bounds__(WG) void mmqi_kernel(GemvArgs a) {
                 }
             }
         }
-    }
-    __shared__ int ctr;
-    if (threadIdx.x == 0) ctr = NWV;
-    if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(lds + Lo.zero)[threadIdx.x] = 0u;
-    for (int i = threadIdx.x; i < ntl * JS * 16 * MT; i += WG) part[i] = 0.0f;
-
-    // ---- work: chunks of C >= DT steps (see the head comment)
-    const int items = ntl * S;
-    const int nchunks = (items + C - 1) / C;
-    const int clampi = max(items - 1, 0);
-    int prow[3], pcol[3];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int p = min(lane + 64 * i, 143);
-        prow[i] = p / 9;
-        pcol[i] = p - 9 * prow[i];
-    }
-    int ld_pos = wave * C, ld_end = ld_pos < items ? min(items, ld_pos + C) : -1;
-    int cp_pos = ld_pos, cp_end = max(ld_end, ld_pos);
-    int pend_pos = -1, pend_end = -1, pend_k = 0;
-    int cp_k = wave;
-    Raw f[DT];
-    lds_barrier();
+    };
+    xload(0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < DT; ++j) {
         load_step(f[j], a, S, invS, t0, ld_pos, clampi, prow, pcol);
         ++ld_pos;
     }
+    __builtin_amdgcn_sched_barrier(0);
+    xbuild(0);
+    for (int base = WG; base < tpt; base += WG) {
+        xload(base);
+        xbuild(base);
+    }
+    __shared__ int ctr;
+    if (threadIdx.x == 0) ctr = NWV;
+    if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(lds + Lo.zero)[threadIdx.x] = 0u;
+    for (int i = threadIdx.x; i < ntl * JS * 16 * MT; i += WG) part[i] = 0.0f;
+    lds_barrier();  // the weight loads stay in flight
     if (ld_end >= 0 && ld_pos > ld_end) ld_end = -1;
 
     auto load_next = [&](Raw& rb) {
@@ -227,7 +250,7 @@ __global__ __launch_bounds__(WG) void mmqi_kernel(GemvArgs a) {
                 }
                 // one 64-element group (two sub-blocks) per iteration, kept
                 // rolled so the operands of one group at a time are live
-#pragma unroll 1
+#pragma unroll JU
                 for (int jj = 0; jj < 4; ++jj) {
                     const fq_u32x2 qs =
                         *reinterpret_cast<const fq_u32x2*>(rowp + 16 + 32 * jj + 8 * q);
