@@ -136,44 +136,51 @@ struct Pk<Q6_K> {
         const uint32_t A[4] = {r.lo.x, r.lo.y, r.lo.z, r.lo.w};
         const uint32_t B[4] = {r.hi.x, r.hi.y, r.hi.z, r.hi.w};
         const uint32_t H[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-        int D[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+        // Group g (quants q1 .. q4 of the dword) sums E_g = D1 2^14 + D2 2^7 + D3
+        // over its 16 elements in one int32 chain: the limb-1 dots, a shift by
+        // 7, the limb-2 dots on top, a shift, the limb-3 dots.  With q <= 63,
+        // |a1| <= 127 and |a2|, |a3| <= 64: |E_g| <= 16 * 63 * (127 * 2^14 +
+        // 64 * 2^7 + 64) < 2^31.
+        int q[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int q1 = (int)((A[i] & 0x0F0F0F0Fu) | ((H[i] & 0x03030303u) << 4));
-            const int q2 = (int)((B[i] & 0x0F0F0F0Fu) | ((H[i] & 0x0C0C0C0Cu) << 2));
-            const int q3 = (int)(((A[i] >> 4) & 0x0F0F0F0Fu) | (H[i] & 0x30303030u));
-            const int q4 = (int)(((B[i] >> 4) & 0x0F0F0F0Fu) | ((H[i] >> 2) & 0x30303030u));
+            q[0][i] = (int)((A[i] & 0x0F0F0F0Fu) | ((H[i] & 0x03030303u) << 4));
+            q[1][i] = (int)((B[i] & 0x0F0F0F0Fu) | ((H[i] & 0x0C0C0C0Cu) << 2));
+            q[2][i] = (int)(((A[i] >> 4) & 0x0F0F0F0Fu) | (H[i] & 0x30303030u));
+            q[3][i] = (int)(((B[i] >> 4) & 0x0F0F0F0Fu) | ((H[i] >> 2) & 0x30303030u));
+        }
+        float E[4];
 #pragma unroll
-            for (int l = 0; l < 3; ++l) {
-                const int* la = l == 0 ? L[0].l1 : l == 1 ? L[0].l2 : L[0].l3;
-                const int* lb = l == 0 ? L[1].l1 : l == 1 ? L[1].l2 : L[1].l3;
-                D[l][0] = sdot4(q1, la[i], D[l][0]);
-                D[l][1] = sdot4(q2, la[4 + i], D[l][1]);
-                D[l][2] = sdot4(q3, lb[i], D[l][2]);
-                D[l][3] = sdot4(q4, lb[4 + i], D[l][3]);
-            }
+        for (int g = 0; g < 4; ++g) {
+            const Limbs& Lg = L[g >> 1];
+            const int o = 4 * (g & 1);
+            int e = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e = sdot4(q[g][i], Lg.l1[o + i], e);
+            e <<= 7;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e = sdot4(q[g][i], Lg.l2[o + i], e);
+            e <<= 7;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e = sdot4(q[g][i], Lg.l3[o + i], e);
+            E[g] = (float)e;  // rounding: 2^-24 relative
         }
         const int h = v & 1;  // sub-scale index l/16 = h: sc[8n + h + 2g]
-        int sc[4];
+        float sc[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int t = h + 2 * g;
             const uint32_t word = t < 4 ? r.sc.x : r.sc.y;
-            sc[g] = (int)(int8_t)((word >> (8 * (t & 3))) & 0xFFu);
+            sc[g] = (float)(int)(int8_t)((word >> (8 * (t & 3))) & 0xFFu);
         }
-        int Ea[3], Eb[3];
-#pragma unroll
-        for (int l = 0; l < 3; ++l) {
-            Ea[l] = __mul24(sc[0], D[l][0]) + __mul24(sc[1], D[l][1]);
-            Eb[l] = __mul24(sc[2], D[l][2]) + __mul24(sc[3], D[l][3]);
-        }
-        float sS = (float)sc[0] * L[0].S[0];
-        sS = __builtin_fmaf((float)sc[1], L[0].S[1], sS);
-        sS = __builtin_fmaf((float)sc[2], L[1].S[0], sS);
-        sS = __builtin_fmaf((float)sc[3], L[1].S[1], sS);
-        const float P = __builtin_fmaf(L[1].s1, limb_sum(Eb[0], Eb[1], Eb[2]),
-                                       L[0].s1 * limb_sum(Ea[0], Ea[1], Ea[2]));
-        return f16_hw(r.d) * __builtin_fmaf(-32.0f, sS, P);
+        float sS = sc[0] * L[0].S[0];
+        sS = __builtin_fmaf(sc[1], L[0].S[1], sS);
+        sS = __builtin_fmaf(sc[2], L[1].S[0], sS);
+        sS = __builtin_fmaf(sc[3], L[1].S[1], sS);
+        const float Ea = __builtin_fmaf(sc[1], E[1], sc[0] * E[0]);
+        const float Eb = __builtin_fmaf(sc[3], E[3], sc[2] * E[2]);
+        const float P = __builtin_fmaf(L[1].s1, Eb, L[0].s1 * Ea);
+        return f16_hw(r.d) * __builtin_fmaf(0x1p-14f, P, -32.0f * sS);
     }
 };
 
