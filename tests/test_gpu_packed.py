@@ -102,3 +102,23 @@ def test_packed_alignment_and_shape_errors():
     assert st == _lib.FQ_ERR_ALIGN
     st = L.fq_pack_weights(F.Q4_0, W.data.data_ptr(), buf.data_ptr(), 8, 480, None)
     assert st == _lib.FQ_ERR_SHAPE
+
+
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_gemv_packed_q6k_limb_chain_extremes(sign):
+    # every 6-bit code at 63 and every activation at 1.99 (limbs a1 = 127,
+    # a2 = 46): each 16-quant group's int32 limb chain reaches ~2.10e9, just
+    # under 2^31; each row's sub-scales all at one int8 extreme
+    N, K = 64, 3584
+    f = F.fmt(F.Q6_K)
+    w = synth.make_weights(F.Q6_K, N, K, seed=41).reshape(N, K // 256, f.block_bytes)
+    w[:, :, 0:192] = 0xFF                                   # ql, qh: q = 63
+    w[0::2, :, 192:208] = np.uint8(127)                      # sub-scales +127
+    w[1::2, :, 192:208] = np.array([-128], np.int8).view(np.uint8)[0]  # and -128
+    w = w.reshape(N, -1)
+    x = np.full((1, K), sign * 1.99, np.float32)
+    P = ops.pack_weights(ops.QWeight.from_numpy(w, F.Q6_K, N, K, device=DEV))
+    y = ops.gemv_packed(torch.from_numpy(x).to(DEV), P).cpu().numpy()
+    y64 = oracle.matmul_f64(F.Q6_K, x, w, N, K)
+    wmax = float(np.max(np.abs(oracle.dequant(F.Q6_K, w, N, K))))
+    assert_close(y[None, :], y64, x, np.array([wmax]), f"q6_k extremes sign {sign}")
