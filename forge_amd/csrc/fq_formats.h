@@ -708,41 +708,43 @@ template <>
 __device__ __forceinline__ float limb_dot<Q6_K>(const Fmt<Q6_K>::Raw& r, int u, const Limbs& L) {
     const uint32_t a[2] = {r.ql_lo.x, r.ql_lo.y}, b[2] = {r.ql_hi.x, r.ql_hi.y},
                    h[2] = {r.qh.x, r.qh.y};
-    int D[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+    int q[4][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int q1 = (int)((a[i] & 0x0F0F0F0Fu) | ((h[i] & 0x03030303u) << 4));
-        const int q2 = (int)((b[i] & 0x0F0F0F0Fu) | ((h[i] & 0x0C0C0C0Cu) << 2));
-        const int q3 = (int)(((a[i] >> 4) & 0x0F0F0F0Fu) | (h[i] & 0x30303030u));
-        const int q4 = (int)(((b[i] >> 4) & 0x0F0F0F0Fu) | ((h[i] >> 2) & 0x30303030u));
-        acc_dword<4>(q1, 0 + i, L, D, 0);
-        acc_dword<4>(q2, 2 + i, L, D, 1);
-        acc_dword<4>(q3, 4 + i, L, D, 2);
-        acc_dword<4>(q4, 6 + i, L, D, 3);
+        q[0][i] = (int)((a[i] & 0x0F0F0F0Fu) | ((h[i] & 0x03030303u) << 4));
+        q[1][i] = (int)((b[i] & 0x0F0F0F0Fu) | ((h[i] & 0x0C0C0C0Cu) << 2));
+        q[2][i] = (int)(((a[i] >> 4) & 0x0F0F0F0Fu) | (h[i] & 0x30303030u));
+        q[3][i] = (int)(((b[i] >> 4) & 0x0F0F0F0Fu) | ((h[i] >> 2) & 0x30303030u));
     }
-    // fold the int8 sub-scales in integer arithmetic: |sum_g sc_g D_g| < 2^24
+    // Group g (slots 8g .. 8g+7) sums E_g = D1 2^14 + D2 2^7 + D3 in one int32
+    // chain: limb-1 dots, shift by 7, limb-2 dots, shift, limb-3 dots.  With
+    // q <= 63, |a1| <= 127, |a2|, |a3| <= 64: |E_g| <= 8 * 63 * (127 * 2^14 +
+    // 64 * 2^7 + 64) < 2^30.
+    float E[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        int e = sdot4(q[g][1], L.l1[2 * g + 1], sdot4(q[g][0], L.l1[2 * g], 0));
+        e = sdot4(q[g][1], L.l2[2 * g + 1], sdot4(q[g][0], L.l2[2 * g], e << 7));
+        e = sdot4(q[g][1], L.l3[2 * g + 1], sdot4(q[g][0], L.l3[2 * g], e << 7));
+        E[g] = (float)e;  // rounding: 2^-24 relative
+    }
     const int is = (u & 3) >> 1;
-    int sc[4];
+    float sc[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const int t = is + 2 * g;
         const uint32_t word = t < 4 ? r.sc.x : r.sc.y;
-        sc[g] = (int)(int8_t)((word >> (8 * (t & 3))) & 0xFFu);
+        sc[g] = (float)(int)(int8_t)((word >> (8 * (t & 3))) & 0xFFu);
     }
-    int E[3];
-    float sS = 0.0f;
+    float P = sc[0] * E[0], sS = sc[0] * L.S[0];
 #pragma unroll
-    for (int l = 0; l < 3; ++l) {
-        int e = 0;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) e = __mul24(sc[g], D[l][g]) + e;
-        E[l] = e;
+    for (int g = 1; g < 4; ++g) {
+        P = __builtin_fmaf(sc[g], E[g], P);
+        sS = __builtin_fmaf(sc[g], L.S[g], sS);
     }
-#pragma unroll
-    for (int g = 0; g < 4; ++g) sS = __builtin_fmaf((float)sc[g], L.S[g], sS);
     const float d = f16_hw(r.d);
     // d * sum_g sc_g (P_g - 32 S_g)
-    return d * __builtin_fmaf(L.s1, limb_sum(E[0], E[1], E[2]), -32.0f * sS);
+    return d * __builtin_fmaf(L.s1 * 0x1p-14f, P, -32.0f * sS);
 }
 
 // 5-bit nibble formats (Q5_0, Q5_1): one group; |sum| <= 32 * 127 * 31.
