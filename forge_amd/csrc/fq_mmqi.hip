@@ -125,7 +125,6 @@ __global__ __launch_bounds__(WG) void mmqi_kernel(GemvArgs a) {
     float* wv = reinterpret_cast<float*>(panel + Layout::PANEL);
     float* part = reinterpret_cast<float*>(lds + Lo.part);
 
-    // ---- activations -> B staging (limbs), per-token sub-block scales and sums
     // ---- work: chunks of C >= DT steps (see the head comment)
     const int items = ntl * S;
     const int nchunks = (items + C - 1) / C;
