@@ -100,6 +100,10 @@ hipError_t scratch(int dev, hipStream_t st, size_t bytes, uint8_t** out, int slo
     return hipSuccess;
 }
 
+int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
+                const void* w3_packed, int n1, int n2, int mode, const float* bias,
+                int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf);
+
 // M > 1 on the matrix cores: token operand preparation, then one tile per
 // work-group (K-split when the tiles alone do not fill the chip).
 int run_mmq(uint32_t dtype, const Geometry& g, const float* x, const void* w, const float* bias,
@@ -171,6 +175,16 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         // a zero-length contraction: y = 0 (with a bias the kernel writes y = bias)
         e = fq::launch_zero(reinterpret_cast<uint32_t*>(y), (size_t)M * N, di.cus, st);
         return e == hipSuccess ? FQ_OK : hip_fail(e);
+    }
+
+    if (M == 1 && K > 0 && packable(dtype)) {
+        // batch 1 on the five benchmark formats: the aligned-layout kernel,
+        // reading the GGUF rows through per-wave LDS buffers (with one token a
+        // full [1][N] bias is a row vector of N)
+        const int rc = packed_gemv(dtype, x, w, nullptr, nullptr, 0, 0, 0,
+                                   bias_mode ? bias : nullptr, bias_mode == 2 ? N : bias_len, y,
+                                   K, N, st, true);
+        if (rc != FQ_ERR_SHAPE) return rc;
     }
 
     if ((M == 1 || M == 2) && K > 0) {
@@ -304,17 +318,21 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
 // gate/up): y[n] = silu(x . w[n]) * (x . w2[n]), run as one GEMV over 2 N
 // interleaved rows.  mode 2 (fused QKV): y = [x . w | x . w2 | x . w3] with
 // n1 and n2 rows in w and w2 and N rows in all.
+// gguf: the same kernel over the unmodified GGUF rows (mode 0 only; the
+// caller has validated the arguments as run_matmul does).
 int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
                 const void* w3_packed, int n1, int n2, int mode, const float* bias,
-                int64_t bias_len, float* y, int K, int N, hipStream_t st) {
+                int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf) {
     Geometry g;
     if (!geometry(dtype, g) || !packable(dtype)) return FQ_ERR_DTYPE;
-    if (N < 0 || K < 0 || K % 256 != 0) return FQ_ERR_SHAPE;
+    if (N < 0 || K < 0 || K % (gguf ? g.be : 256) != 0) return FQ_ERR_SHAPE;
     if (N == 0) return FQ_OK;
     if (!x || !w_packed || !y) return FQ_ERR_NULL;
-    if ((reinterpret_cast<uintptr_t>(w_packed) & 15) != 0) return FQ_ERR_ALIGN;
+    if (gguf && mode != 0) return FQ_ERR_SHAPE;
+    const uintptr_t amask = gguf ? 1 : 15;
+    if ((reinterpret_cast<uintptr_t>(w_packed) & amask) != 0) return FQ_ERR_ALIGN;
     for (const void* p : {w2_packed, w3_packed})
-        if (p && (reinterpret_cast<uintptr_t>(p) & 15) != 0) return FQ_ERR_ALIGN;
+        if (p && (reinterpret_cast<uintptr_t>(p) & amask) != 0) return FQ_ERR_ALIGN;
     const bool dual = mode == 1;
     const int NV = dual ? 2 * N : N;  // rows the kernel walks
     int dev = 0;
@@ -330,23 +348,34 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     fq::gemvp_geometry((int)dtype, K, &units, &records);
     size_t lds = 0;
     int wg = 0;
+    const size_t lds_cap = std::min<size_t>(di.lds, 160 * 1024);
+    // partial sums a work-group can buffer: a static 4096-entry array for the
+    // packed kernel, the LDS left after the records and wave buffers for GGUF
+    long pcap = 4096;
     const void* fn =
-        fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, mode);
-    if (!fn || lds > std::min<size_t>(di.lds, 160 * 1024)) return FQ_ERR_SHAPE;
+        gguf ? fq::gemvg_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg)
+             : fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, mode);
+    if (gguf) {
+        if (lds + 64 * 4 > lds_cap) return FQ_ERR_SHAPE;
+        pcap = std::min<long>(4096, (long)(lds_cap - lds) / 4);
+    }
+    if (!fn || lds > lds_cap) return FQ_ERR_SHAPE;
     int per_cu = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wg, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wg,
+                                                     gguf ? lds + 4 * pcap : lds);
     if (e != hipSuccess) return hip_fail(e);
     if (per_cu < 1) return FQ_ERR_SHAPE;
     const int wpb = wg / 64;
     // one work-group per resident slot, each owning a contiguous row range
     // with at least one row per wave, and whose row x K-slice partial sums fit
-    // its 4096-entry LDS buffer (slices of 64 lane units)
+    // its LDS buffer (slices of 64 lane units)
     const long ns = (units + 63) / 64;
     long G = (long)di.cus * per_cu;
     G = std::max(1L, std::min<long>(G, ((long)NV + wpb - 1) / wpb));
     auto max_rows = [&](long g) { return dual ? 2 * ((N + g - 1) / g) : (NV + g - 1) / g; };
-    G = std::max<long>(G, ((long)NV * ns + 4095) / 4096);
-    while (max_rows(G) * ns > 4096) ++G;
+    G = std::max<long>(G, ((long)NV * ns + pcap - 1) / pcap);
+    while (max_rows(G) * ns > pcap) ++G;
+    if (gguf) lds += 4 * (size_t)(max_rows(G) * ns);
     fq::GemvArgs a{};
     a.x = x;
     a.w = static_cast<const uint8_t*>(w_packed);
@@ -363,7 +392,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     a.N = NV;
     a.U = units;
     a.Uc = records;
-    a.row_bytes = (int)fq::packed_row_bytes((int)dtype, K);
+    a.row_bytes = gguf ? (K / g.be) * g.bb : (int)fq::packed_row_bytes((int)dtype, K);
     e = fq::launch_raw(fn, a, (int)G, wg, lds, st);
     return e == hipSuccess ? FQ_OK : hip_fail(e);
 }
@@ -484,14 +513,14 @@ int fq_unpack_weights(uint32_t dtype, const void* w_packed, void* w_gguf, int N,
 int fq_gemv_packed(uint32_t dtype, const float* x, const void* w_packed, const float* bias,
                    int64_t bias_len, float* y, int K, int N, void* stream) {
     return packed_gemv(dtype, x, w_packed, nullptr, nullptr, 0, 0, 0, bias, bias_len, y, K, N,
-                       static_cast<hipStream_t>(stream));
+                       static_cast<hipStream_t>(stream), false);
 }
 
 int fq_ffn_up_fused_packed(uint32_t dtype, const float* x, const void* w_gate_packed,
                            const void* w_up_packed, float* y, int K, int N, void* stream) {
     if (!w_up_packed) return FQ_ERR_NULL;
     return packed_gemv(dtype, x, w_gate_packed, w_up_packed, nullptr, 0, 0, 1, nullptr, 0, y, K,
-                       N, static_cast<hipStream_t>(stream));
+                       N, static_cast<hipStream_t>(stream), false);
 }
 
 int fq_fused_qkv_packed(uint32_t dtype, const float* x, const void* wq, const void* wk,
@@ -499,7 +528,7 @@ int fq_fused_qkv_packed(uint32_t dtype, const float* x, const void* wq, const vo
     if (Nq < 0 || Nk < 0 || Nv < 0 || (int64_t)Nq + Nk + Nv > INT32_MAX) return FQ_ERR_SHAPE;
     if ((Nk && !wk) || (Nv && !wv)) return FQ_ERR_NULL;
     return packed_gemv(dtype, x, wq, wk, wv, Nq, Nk, 2, nullptr, 0, y, K, Nq + Nk + Nv,
-                       static_cast<hipStream_t>(stream));
+                       static_cast<hipStream_t>(stream), false);
 }
 
 int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk, const void* wv,
@@ -558,7 +587,7 @@ int fq_ffn_down_residual_packed(uint32_t dtype, const float* x, const void* w_pa
                                 const float* residual, float* y, int K, int N, void* stream) {
     if (!residual) return FQ_ERR_NULL;
     return packed_gemv(dtype, x, w_packed, nullptr, nullptr, 0, 0, 0, residual, N, y, K, N,
-                       static_cast<hipStream_t>(stream));
+                       static_cast<hipStream_t>(stream), false);
 }
 
 int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const void* w_up, float* y,

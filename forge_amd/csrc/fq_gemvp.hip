@@ -184,6 +184,81 @@ struct Pk<Q6_K> {
     }
 };
 
+// ---- GGUF rows.  The same lane units, read from the reference's unmodified
+// block bytes.  A wave fetches the 16-byte-aligned superset of one K-slice
+// (64 lane units) of one row with coalesced dwordx4 loads (lane p loads piece
+// p, so each load instruction covers 1 KiB of contiguous HBM), writes the
+// pieces to its own LDS buffer and every lane then reads its unit at the
+// block layout's offsets, which are only 2-byte aligned (LDS reads on gfx950
+// need no alignment).  Fetching the aligned superset never crosses a page.
+// BB: block bytes; UPB: lane units per block.
+template <int F>
+struct Gk;
+
+template <>
+struct Gk<Q4_0> {  // d @0, qs[16] @2
+    static constexpr int BB = 18, UPB = 1;
+    __device__ static Pk<Q4_0>::Raw read(const uint8_t* s, int u) {
+        const uint8_t* b = s + 18 * u;
+        return {ld_u16(b), ld_u128(b + 2)};
+    }
+};
+
+template <>
+struct Gk<Q4_1> {  // d @0, m @2, qs[16] @4
+    static constexpr int BB = 20, UPB = 1;
+    __device__ static Pk<Q4_1>::Raw read(const uint8_t* s, int u) {
+        const uint8_t* b = s + 20 * u;
+        return {ld_u32(b), ld_u128(b + 4)};
+    }
+};
+
+template <>
+struct Gk<Q8_0> {  // d @0, qs[32] @2
+    static constexpr int BB = 34, UPB = 1;
+    __device__ static Pk<Q8_0>::Raw read(const uint8_t* s, int u) {
+        const uint8_t* b = s + 34 * u;
+        return {ld_u16(b), ld_u128(b + 2), ld_u128(b + 18)};
+    }
+};
+
+template <>
+struct Gk<Q4_K> {  // d dmin scales[12] @0, qs[128] @16; unit u = 4 s + g
+    static constexpr int BB = 144, UPB = 4;
+    __device__ static Q4KP read(const uint8_t* s, int u) {
+        const uint8_t* b = s + 144 * (u >> 2);
+        const int g = u & 3;
+        return {ld_u128(b), ld_u128(b + 16 + 32 * g), ld_u128(b + 32 + 32 * g)};
+    }
+};
+
+template <>
+struct Gk<Q6_K> {  // ql[128] @0, qh[64] @128, sc[16] @192, d @208; unit u = 4 s + 2 n + h
+    static constexpr int BB = 210, UPB = 4;
+    __device__ static Q6P read(const uint8_t* s, int u) {
+        const uint8_t* b = s + 210 * (u >> 2);
+        const int n = (u >> 1) & 1, h = u & 1;
+        return {ld_u128(b + 64 * n + 16 * h), ld_u128(b + 64 * n + 32 + 16 * h),
+                ld_u128(b + 128 + 32 * n + 16 * h), ld_u64(b + 192 + 8 * n), ld_u16(b + 208)};
+    }
+};
+
+// Bytes of one K-slice (64 lane units) of a GGUF row, and the dwordx4 pieces
+// per lane that cover its aligned superset (at most 14 bytes of misalignment).
+template <int F>
+constexpr int slice_bytes() {
+    return 64 / Gk<F>::UPB * Gk<F>::BB;
+}
+template <int F>
+constexpr int slice_pieces(int units) {
+    return ((units / Gk<F>::UPB * Gk<F>::BB + 14 + 15) / 16 + 63) / 64;
+}
+
+template <int GP>
+struct Pieces {
+    uint4 v[GP];
+};
+
 // Work distribution.  Work-group g owns the contiguous rows [lo, hi) =
 // [N g / G, N (g+1) / G).  Its work is the sequence of (K-slice, row) steps
 // in slice-major order, f = s * rows + r (a K-slice is 64 lane units), cut
@@ -251,13 +326,44 @@ __device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int v) {
     return a.w + (size_t)v * a.row_bytes;
 }
 
-template <int F, int NL, int MODE = ONE>
-__device__ __forceinline__ void pload(typename Pk<F>::Raw (&f)[NL], const GemvArgs& a,
+// Per-step weight registers: the lane's packed unit (GP = 0), or GP pieces of
+// the aligned superset of a GGUF K-slice.
+template <int F, int GP>
+struct RegSel {
+    using T = Pieces<GP>;
+};
+template <int F>
+struct RegSel<F, 0> {
+    using T = typename Pk<F>::Raw;
+};
+
+// First byte of step t's K-slice in a GGUF row.
+template <int F, int MODE>
+__device__ __forceinline__ const uint8_t* gslice(const GemvArgs& a, const It& t, int lo) {
+    return row_ptr<MODE>(a, min(lo + t.r, a.N - 1)) + (size_t)t.s * slice_bytes<F>();
+}
+
+template <int F, int NL, int MODE, int GP>
+__device__ __forceinline__ void pload(typename RegSel<F, GP>::T (&f)[NL], const GemvArgs& a,
                                       const It& t, int lo, int lane) {
-    const uint8_t* r = row_ptr<MODE>(a, min(lo + t.r, a.N - 1));
-    const int v0 = t.s * 64 * NL;
+    if constexpr (GP == 0) {
+        const uint8_t* r = row_ptr<MODE>(a, min(lo + t.r, a.N - 1));
+        const int v0 = t.s * 64 * NL;
 #pragma unroll
-    for (int c = 0; c < NL; ++c) f[c] = Pk<F>::load(r, min(v0 + lane + 64 * c, a.U - 1), a.U);
+        for (int c = 0; c < NL; ++c)
+            f[c] = Pk<F>::load(r, min(v0 + lane + 64 * c, a.U - 1), a.U);
+    } else {
+        static_assert(NL == 1, "GGUF slices are 64 lane units");
+        // pointer arithmetic (not integer casts) keeps the global address
+        // space, so these stay global_load (vmcnt only)
+        const uint8_t* g0 = gslice<F, MODE>(a, t, lo);
+        const int shift = (int)(reinterpret_cast<uintptr_t>(g0) & 15);
+        const uint8_t* a0 = g0 - shift;
+        const int units = min(64, a.U - 64 * t.s);
+        const int n16 = (shift + units / Gk<F>::UPB * Gk<F>::BB + 15) >> 4;
+#pragma unroll
+        for (int i = 0; i < GP; ++i) f[0].v[i] = ldg128<true>(a0 + 16 * min(lane + 64 * i, n16 - 1));
+    }
 }
 
 template <int F, int NL>
@@ -281,11 +387,16 @@ __device__ __forceinline__ void advance_load(It& ld, It& q, const Claims& cl, in
 
 // One step of the compute side (slice cp.s of row lo + cp.r), then the loads
 // of the load side's step into the same registers.
-template <int F, int NL, int D, bool BIAS, int MODE>
-__device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& ld, It& q,
+// GGUF (GP > 0): the step's pieces go to the wave's LDS buffer wbuf first,
+// the next loads are issued into the freed registers, then each lane reads
+// its unit from the buffer.  A wave's LDS accesses execute in order, so no
+// barrier separates the writes from the reads.
+template <int F, int NL, int D, bool BIAS, int MODE, int GP>
+__device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], It& cp, It& ld, It& q,
                                       const Claims& cl, const GemvArgs& a,
                                       Limbs (&L)[NL][Pk<F>::NREC], const uint8_t* lds,
-                                      float* part, int lo, int lane, int& cur_s, float& res) {
+                                      uint8_t* wbuf, float* part, int lo, int lane, int& cur_s,
+                                      float& res) {
     __builtin_amdgcn_sched_barrier(0);
     if (cp.s != cur_s) {  // wave-uniform
         load_slice_limbs<F, NL>(L, lds, cp.s, a.U, lane);
@@ -293,21 +404,26 @@ __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& 
     }
     const int v0 = cp.s * 64 * NL;
     float acc = 0.0f;
+    if constexpr (GP == 0) {
 #pragma unroll
-    for (int c = 0; c < NL; ++c) {
-        const int v = v0 + lane + 64 * c;
-        const float t = Pk<F>::dot(f[c], min(v, a.U - 1), L[c]);
-        acc += v < a.U ? t : 0.0f;
-    }
-    pload<F, NL, MODE>(f, a, ld, lo, lane);
-    float s = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
-    if constexpr (BIAS) {
-        if (cp.s == 0) {
-            const int r = lo + cp.r;
-            s += r < a.bias_len ? ((const_fp)(uintptr_t)a.bias)[r] : 0.0f;
+        for (int c = 0; c < NL; ++c) {
+            const int v = v0 + lane + 64 * c;
+            const float t = Pk<F>::dot(f[c], min(v, a.U - 1), L[c]);
+            acc += v < a.U ? t : 0.0f;
         }
+        pload<F, NL, MODE, GP>(f, a, ld, lo, lane);
+    } else {
+#pragma unroll
+        for (int i = 0; i < GP; ++i) reinterpret_cast<uint4*>(wbuf)[lane + 64 * i] = f[0].v[i];
+        const int shift = (int)(reinterpret_cast<uintptr_t>(gslice<F, MODE>(a, cp, lo)) & 15);
+        const int v = v0 + lane;
+        const auto raw = Gk<F>::read(wbuf + shift, min(v, a.U - 1) - v0);
+        pload<F, NL, MODE, GP>(f, a, ld, lo, lane);
+        const float t = Pk<F>::dot(raw, min(v, a.U - 1), L[0]);
+        acc = v < a.U ? t : 0.0f;
     }
+    const float s = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
     // advance the compute side; a finished item goes to the LDS partial buffer
     if (cp.n > 0) {  // wave-uniform; past the last item the step only keeps the loads in step
         res = lane == cp.k ? res + s : res;
@@ -327,13 +443,25 @@ __device__ __forceinline__ void pstep(typename Pk<F>::Raw (&f)[NL], It& cp, It& 
 // MODE PAIR: y[n] = silu(x . w[n]) * (x . w2[n]) over a.N = 2 N virtual
 // rows (the fused FFN gate and up projections); work-group row ranges are
 // even.  MODE CAT: y is the concatenation of the three GEMVs (fused QKV).
-template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE>
+// GP > 0: GGUF rows, GP pieces per lane per K-slice; the dynamic LDS holds
+// the limb records, then one GP KiB buffer per wave, then the partial sums
+// (sized by the host).
+template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE, int GP = 0>
 __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     constexpr bool DUAL = MODE == PAIR;
     static_assert(D <= CR, "an item must span at least D steps");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int ctr;
-    __shared__ float part[YBUF];
+    constexpr int W = WG / 64;
+    float* part;
+    uint8_t* wbuf = nullptr;
+    if constexpr (GP == 0) {
+        __shared__ float part_s[YBUF];
+        part = part_s;
+    } else {
+        wbuf = lds + (size_t)a.Uc * RECB + (threadIdx.x >> 6) * (GP * 1024);
+        part = reinterpret_cast<float*>(lds + (size_t)a.Uc * RECB + W * GP * 1024);
+    }
     using P = Pk<F>;
     const int lane = threadIdx.x & 63;
     const int ns = (a.U + 64 * NL - 1) / (64 * NL);
@@ -352,22 +480,21 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     // build, so HBM is busy during the staging without delaying the
     // activations (the remaining first loads follow the barrier: issued all
     // at once they would queue ahead of other work-groups' activation loads)
-    constexpr int W = WG / 64;
     if (threadIdx.x == 0) ctr = W;
     It q{0, 0, 0, 0, 0};
     It ld = item(cl, __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6)), cp = ld;
-    typename P::Raw f[D][NL];
+    typename RegSel<F, GP>::T f[D][NL];
     {
         XStage<P, WG> xs;
         stage_load<P, WG>(xs, a.x, a.Uc, 0);
-        pload<F, NL, MODE>(f[0], a, ld, lo, lane);
+        pload<F, NL, MODE, GP>(f[0], a, ld, lo, lane);
         stage_build<P, WG, false>(lds, xs, a.x, a.Uc, 0);
     }
     lds_barrier();  // the weight loads stay in flight
     advance_load(ld, q, cl, lane);
 #pragma unroll
     for (int j = 1; j < D; ++j) {
-        pload<F, NL, MODE>(f[j], a, ld, lo, lane);
+        pload<F, NL, MODE, GP>(f[j], a, ld, lo, lane);
         advance_load(ld, q, cl, lane);
     }
     Limbs L[NL][P::NREC];
@@ -380,8 +507,8 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     while (cp.n > 0) {
 #pragma unroll
         for (int j = 0; j < D; ++j)
-            pstep<F, NL, D, BIAS, MODE>(f[j], cp, ld, q, cl, a, L, lds, part, lo, lane, cur_s,
-                                        res);
+            pstep<F, NL, D, BIAS, MODE, GP>(f[j], cp, ld, q, cl, a, L, lds, wbuf, part, lo, lane,
+                                            cur_s, res);
     }
     __syncthreads();
     if constexpr (DUAL) {
@@ -394,9 +521,12 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
             a.y[(lo >> 1) + r] = gt / (1.0f + expf(-gt)) * up;  // silu(gate) * up
         }
     } else {
+        // the bias is added to the finished row sum, as apply_bias adds it to
+        // the finished product (matmul.cpp:1005-1049)
         for (int r = threadIdx.x; r < rows; r += WG) {
             float v = part[r];
             for (int s = 1; s < ns; ++s) v += part[s * rows + r];
+            if constexpr (BIAS) v += lo + r < a.bias_len ? a.bias[lo + r] : 0.0f;
             a.y[lo + r] = v;
         }
     }
@@ -420,6 +550,43 @@ template <int F>
 const void* pfn_mode(int mode) {
     return mode == PAIR ? reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WGP, PAIR>)
                         : reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WGP, CAT>);
+}
+
+// GGUF rows: GP pieces per lane cover a K-slice; only the counts a format's
+// slices can need are instantiated.
+template <int F>
+constexpr int max_pieces() {
+    return slice_pieces<F>(64);
+}
+
+// Four pieces per lane need more than the 128 VGPRs of a 1024-thread
+// work-group (D steps of pieces plus the unit and the limbs): 512 threads.
+template <int GP>
+constexpr int gwg() {
+    return GP >= 4 ? 512 : WGP;
+}
+
+template <int F, int GP>
+const void* gfn2(bool bias) {
+    if constexpr (GP > max_pieces<F>()) {
+        return nullptr;
+    } else {
+        constexpr int WG = gwg<GP>();
+        return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, true, WG, ONE, GP>)
+                    : reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WG, ONE, GP>);
+    }
+}
+
+template <int F>
+const void* gfn(int units, bool bias, int* gp) {
+    *gp = slice_pieces<F>(units < 64 ? units : 64);
+    switch (*gp) {
+        case 1: return gfn2<F, 1>(bias);
+        case 2: return gfn2<F, 2>(bias);
+        case 3: return gfn2<F, 3>(bias);
+        case 4: return gfn2<F, 4>(bias);
+        default: return nullptr;
+    }
 }
 
 }  // namespace
@@ -450,6 +617,25 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
     }
     *lds = (size_t)records * RECB;
     *wg = WGP;
+    return fn;
+}
+
+// The same kernel over GGUF rows (K-slices staged through a per-wave LDS
+// buffer).  *lds_fixed: the records and the wave buffers; the host adds the
+// partial-sum buffer after them.
+const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
+                            int* wg) {
+    int gp = 0;
+    const void* fn = nullptr;
+    switch (dtype) {
+        case Q4_0: fn = gfn<Q4_0>(units, bias, &gp); break;
+        case Q4_1: fn = gfn<Q4_1>(units, bias, &gp); break;
+        case Q8_0: fn = gfn<Q8_0>(units, bias, &gp); break;
+        case Q4_K: fn = gfn<Q4_K>(units, bias, &gp); break;
+        case Q6_K: fn = gfn<Q6_K>(units, bias, &gp); break;
+    }
+    *wg = gp >= 4 ? gwg<4>() : WGP;
+    *lds_fixed = (size_t)records * RECB + (size_t)(*wg / 64) * gp * 1024;
     return fn;
 }
 
