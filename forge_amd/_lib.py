@@ -19,6 +19,7 @@ FQ_ERR_NULL = 3
 FQ_ERR_HIP = 4
 FQ_ERR_NO_DEVICE = 5
 FQ_ERR_ALIGN = 6
+FQ_ERR_WORKSPACE = 7
 
 # Every symbol include/forge_q.h declares, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -44,6 +45,8 @@ SIGNATURES = {
     "fq_fused_qkv_packed": (_I, [_U, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "fq_ffn_down_residual": (_I, [_U, _P, _P, _P, _P, _I, _I, _I, _P]),
     "fq_ffn_down_residual_packed": (_I, [_U, _P, _P, _P, _P, _I, _I, _P]),
+    "fq_reserve_workspace": (_I, [_I, _I, _I, _P]),
+    "fq_release_workspace": (_I, [_P]),
 }
 
 _lib = None

@@ -14,6 +14,8 @@
 #include <cstdio>
 #include <cstdint>
 #include <map>
+#include <memory>
+#include <vector>
 #include <tuple>
 #include <mutex>
 #include <utility>
@@ -76,68 +78,122 @@ DevInfo device_info(int dev) {
     return d;
 }
 
-// Grow-only device scratch per (device, stream) for the MFMA path: token
-// operands, group sums, exponents and split-K partial slabs.
-// slot 0: the MFMA path's operands; slot 1: the fused FFN's gate/up rows.
-hipError_t scratch(int dev, hipStream_t st, size_t bytes, uint8_t** out, int slot = 0) {
-    static std::mutex mu;
-    static std::map<std::tuple<int, hipStream_t, int>, std::pair<uint8_t*, size_t>> bufs;
-    std::lock_guard<std::mutex> lk(mu);
-    auto& b = bufs[{dev, st, slot}];
-    if (b.second < bytes) {
-        if (b.first) {
-            hipError_t e = hipStreamSynchronize(st);  // queued work may still read it
-            if (e != hipSuccess) return e;
-            hipFree(b.first);
-            b.first = nullptr;
-            b.second = 0;
+// Device scratch per (device, stream, slot) for the MFMA path (slot 0: token
+// operands, group sums, exponents and split-K partial slabs) and the GGUF
+// fused FFN / QKV (slot 1: the gate/up or per-matrix rows).
+//
+// A call holds its slot's lock (StreamScratch::Lease) from taking the pointer
+// until its launches are enqueued, so two host threads sharing a stream never
+// see a buffer change under them.  The buffer only grows, at least doubling;
+// a superseded buffer is not freed inside a compute call (queued work may
+// still read it, and waiting for it would block the host mid-stream): it is
+// kept until fq_release_workspace(), so the workspace of a stream holds less
+// than twice its largest request.  fq_reserve_workspace() sizes it up front;
+// during HIP-graph capture a call that would have to grow it fails with
+// FQ_ERR_WORKSPACE instead of allocating.
+struct StreamScratch {
+    std::mutex mu;
+    uint8_t* p = nullptr;
+    size_t n = 0;
+    std::vector<uint8_t*> retired;
+
+    class Lease {
+      public:
+        explicit Lease(StreamScratch& s) : lk_(s.mu), s_(s) {}
+        // the slot's buffer, at least `bytes` long
+        int get(size_t bytes, hipStream_t st, uint8_t** out) {
+            if (s_.n < bytes) {
+                hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+                if (st && hipStreamIsCapturing(st, &cs) == hipSuccess &&
+                    cs != hipStreamCaptureStatusNone)
+                    return FQ_ERR_WORKSPACE;
+                const size_t want = std::max(bytes, 2 * s_.n);
+                uint8_t* np = nullptr;
+                const hipError_t e = hipMalloc(reinterpret_cast<void**>(&np), want);
+                if (e != hipSuccess) return hip_fail(e);
+                if (s_.p) s_.retired.push_back(s_.p);
+                s_.p = np;
+                s_.n = want;
+            }
+            *out = s_.p;
+            return FQ_OK;
         }
-        hipError_t e = hipMalloc(reinterpret_cast<void**>(&b.first), bytes);
-        if (e != hipSuccess) return e;
-        b.second = bytes;
-    }
-    *out = b.first;
-    return hipSuccess;
+
+      private:
+        std::unique_lock<std::mutex> lk_;
+        StreamScratch& s_;
+    };
+};
+
+std::mutex g_scratch_mu;
+std::map<std::tuple<int, hipStream_t, int>, std::unique_ptr<StreamScratch>> g_scratch;
+
+StreamScratch& stream_scratch(int dev, hipStream_t st, int slot) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto& p = g_scratch[{dev, st, slot}];
+    if (!p) p.reset(new StreamScratch);
+    return *p;
 }
 
-int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
-                const void* w3_packed, int n1, int n2, int mode, const float* bias,
-                int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf);
+// Workspace bytes of the MFMA path for one call (the same plan run_mmq makes).
+struct MmqPlan {
+    int Tp, NC, shape, gx, gy, splits;
+    size_t xop_b, xsum_b, ex_b, part_b, total;
+};
 
-// M > 1 on the matrix cores: token operand preparation, then one tile per
-// work-group (K-split when the tiles alone do not fill the chip).
-int run_mmq(uint32_t dtype, const Geometry& g, const float* x, const void* w, const float* bias,
-            int bias_mode, int64_t bias_len, float* y, int M, int K, int N, int dev,
-            const DevInfo& di, hipStream_t st) {
-    const int Tp = (M + 15) / 16, NC = (K + 63) / 64;
-    const int shape = Tp == 1 ? fq::MMQ_SMALL1 : Tp == 2 ? fq::MMQ_SMALL2
-                      : Tp <= 4 ? fq::MMQ_MID : fq::MMQ_BIG;
+MmqPlan plan_mmq(int M, int K, int N, int cus) {
+    MmqPlan p{};
+    p.Tp = (M + 15) / 16;
+    p.NC = (K + 63) / 64;
+    p.shape = p.Tp == 1 ? fq::MMQ_SMALL1 : p.Tp == 2 ? fq::MMQ_SMALL2
+              : p.Tp <= 4 ? fq::MMQ_MID : fq::MMQ_BIG;
     int bn = 0, bm = 0;
-    fq::mmq_shape(shape, &bn, &bm);
-    const int gx = (N + bn - 1) / bn, gy = (Tp + bm / 16 - 1) / (bm / 16);
-    const long tiles = (long)gx * gy;
+    fq::mmq_shape(p.shape, &bn, &bm);
+    p.gx = (N + bn - 1) / bn;
+    p.gy = (p.Tp + bm / 16 - 1) / (bm / 16);
+    const long tiles = (long)p.gx * p.gy;
     // K-splits only when the tiles alone leave CUs idle, to about two
     // work-groups per CU for the 128x128 prefill tiles and three for the
     // small-batch tiles (measured: cfg4 448 tiles fastest unsplit, 128 tiles
     // with 4 splits; 18944-row Q5_K at M = 8 41 -> 37 us with 6 splits)
-    const long per_cu = shape == fq::MMQ_BIG ? 2 : 3;
-    int splits = tiles >= di.cus ? 1
-                                 : (int)std::max(1L, std::min<long>((per_cu * di.cus + tiles - 1) / tiles, 8));
-    splits = std::max(1, std::min(splits, NC / 4));
-    const size_t xop_b = (size_t)Tp * NC * 2048 * 2, xsum_b = (size_t)Tp * NC * 64 * 4,
-                 ex_b = (size_t)Tp * NC * 16 * 4;
-    const size_t part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+    const long per_cu = p.shape == fq::MMQ_BIG ? 2 : 3;
+    int splits = tiles >= cus ? 1
+                              : (int)std::max(1L, std::min<long>((per_cu * cus + tiles - 1) / tiles, 8));
+    p.splits = std::max(1, std::min(splits, p.NC / 4));
+    p.xop_b = (size_t)p.Tp * p.NC * 2048 * 2;
+    p.xsum_b = (size_t)p.Tp * p.NC * 64 * 4;
+    p.ex_b = (size_t)p.Tp * p.NC * 16 * 4;
+    p.part_b = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    uint8_t* buf = nullptr;
-    hipError_t e = scratch(dev, st, 256 + al(xop_b) + al(xsum_b) + al(ex_b) + al(part_b), &buf);
-    if (e != hipSuccess) return hip_fail(e);
+    p.total = 256 + al(p.xop_b) + al(p.xsum_b) + al(p.ex_b) + al(p.part_b);
+    return p;
+}
+
+// M > 1 on the matrix cores: token operand preparation, then one tile per
+// work-group (K-split when the tiles alone do not fill the chip).  The
+// workspace is `fixed` (fixed_cap bytes) when given, else the stream's.
+int run_mmq(uint32_t dtype, const Geometry& g, const float* x, const void* w, const float* bias,
+            int bias_mode, int64_t bias_len, float* y, int M, int K, int N, int dev,
+            const DevInfo& di, hipStream_t st, uint8_t* fixed, size_t fixed_cap) {
+    const MmqPlan pl = plan_mmq(M, K, N, di.cus);
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    std::unique_ptr<StreamScratch::Lease> lease;
+    uint8_t* buf = fixed;
+    if (fixed) {
+        if (pl.total > fixed_cap) return FQ_ERR_WORKSPACE;
+    } else {
+        lease.reset(new StreamScratch::Lease(stream_scratch(dev, st, 0)));
+        const int rc = lease->get(pl.total, st, &buf);
+        if (rc != FQ_OK) return rc;
+    }
     fq::MmqArgs a{};
     a.w = static_cast<const uint8_t*>(w);
     a.xop = buf;
-    a.xsum = reinterpret_cast<const float*>(buf + al(xop_b));
-    a.ex = reinterpret_cast<const int*>(buf + al(xop_b) + al(xsum_b));
-    a.part = splits > 1 ? reinterpret_cast<float*>(buf + al(xop_b) + al(xsum_b) + al(ex_b))
-                        : nullptr;
+    a.xsum = reinterpret_cast<const float*>(buf + al(pl.xop_b));
+    a.ex = reinterpret_cast<const int*>(buf + al(pl.xop_b) + al(pl.xsum_b));
+    a.part = pl.splits > 1
+                 ? reinterpret_cast<float*>(buf + al(pl.xop_b) + al(pl.xsum_b) + al(pl.ex_b))
+                 : nullptr;
     a.y = y;
     a.bias = bias;
     a.bias_len = bias_mode ? bias_len : 0;
@@ -145,19 +201,29 @@ int run_mmq(uint32_t dtype, const Geometry& g, const float* x, const void* w, co
     a.M = M;
     a.N = N;
     a.K = K;
-    a.NC = NC;
+    a.NC = pl.NC;
     a.row_bytes = (K / g.be) * g.bb;
-    if (NC > 0) {  // K == 0 only writes the bias (or zeros)
-        e = fq::launch_xprep((int)dtype, x, M, K, NC, reinterpret_cast<_Float16*>(buf),
+    hipError_t e = hipSuccess;
+    if (pl.NC > 0) {  // K == 0 only writes the bias (or zeros)
+        e = fq::launch_xprep((int)dtype, x, M, K, pl.NC, reinterpret_cast<_Float16*>(buf),
                              const_cast<float*>(a.xsum), const_cast<int*>(a.ex), st);
         if (e != hipSuccess) return hip_fail(e);
     }
-    e = fq::launch_mmq((int)dtype, a, shape, gx, gy, splits, st);
+    e = fq::launch_mmq((int)dtype, a, pl.shape, pl.gx, pl.gy, pl.splits, st);
     return e == hipSuccess ? FQ_OK : hip_fail(e);
 }
 
 int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias, int bias_mode,
-               int64_t bias_len, float* y, int M, int K, int N, hipStream_t st) {
+               int64_t bias_len, float* y, int M, int K, int N, hipStream_t st,
+               uint8_t* fixed = nullptr, size_t fixed_cap = 0);
+
+int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
+                const void* w3_packed, int n1, int n2, int mode, const float* bias,
+                int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf);
+
+int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias, int bias_mode,
+               int64_t bias_len, float* y, int M, int K, int N, hipStream_t st, uint8_t* fixed,
+               size_t fixed_cap) {
     Geometry g;
     if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
     if (M < 0 || N < 0 || K < 0) return FQ_ERR_SHAPE;
@@ -314,7 +380,8 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     }
 
     // M > 4, and rows too long for the batch-1 kernels' LDS
-    return run_mmq(dtype, g, x, w, bias, bias_mode, bias_len, y, M, K, N, dev, di, st);
+    return run_mmq(dtype, g, x, w, bias, bias_mode, bias_len, y, M, K, N, dev, di, st, fixed,
+                   fixed_cap);
 }
 
 // Batch-1 GEMV over packed rows.  mode 0: y = x . w (+ bias).  mode 1 (fused
@@ -421,6 +488,9 @@ const char* fq_status_str(int status) {
         case FQ_ERR_HIP: return "HIP runtime error";
         case FQ_ERR_NO_DEVICE: return "no HIP device";
         case FQ_ERR_ALIGN: return "packed buffer not 16-byte aligned";
+        case FQ_ERR_WORKSPACE:
+            return "workspace too small (reserve it with fq_reserve_workspace before graph "
+                   "capture)";
         default: return "unknown status";
     }
 }
@@ -563,8 +633,9 @@ int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk,
     const DevInfo di = device_info(dev);
     uint8_t* buf = nullptr;
     const int nmax = std::max(Nq, std::max(Nk, Nv));
-    e = scratch(dev, st, (size_t)M * nmax * sizeof(float), &buf, 1);
-    if (e != hipSuccess) return hip_fail(e);
+    StreamScratch::Lease lease(stream_scratch(dev, st, 1));
+    const int rs = lease.get((size_t)M * nmax * sizeof(float), st, &buf);
+    if (rs != FQ_OK) return rs;
     float* tmp = reinterpret_cast<float*>(buf);
     int off = 0;
     for (int i = 0; i < 3; ++i) {
@@ -606,8 +677,9 @@ int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const vo
     if (e != hipSuccess) return hip_fail(e);
     const DevInfo di = device_info(dev);
     uint8_t* buf = nullptr;
-    e = scratch(dev, st, 2 * (size_t)M * N * sizeof(float), &buf, 1);
-    if (e != hipSuccess) return hip_fail(e);
+    StreamScratch::Lease lease(stream_scratch(dev, st, 1));
+    const int rs = lease.get(2 * (size_t)M * N * sizeof(float), st, &buf);
+    if (rs != FQ_OK) return rs;
     float* gate = reinterpret_cast<float*>(buf);
     float* up = gate + (size_t)M * N;
     int rc = run_matmul(dtype, x, w_gate, nullptr, 0, 0, gate, M, K, N, st);
@@ -616,6 +688,51 @@ int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const vo
     if (rc != FQ_OK) return rc;
     e = fq::launch_silu_mul(gate, up, y, (size_t)M * N, di.cus, st);
     return e == hipSuccess ? FQ_OK : hip_fail(e);
+}
+
+int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
+    if (M_max < 0 || K_max < 0 || N_max < 0) return FQ_ERR_SHAPE;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    const DevInfo di = device_info(dev);
+    // slot 0: the largest MFMA-path plan for up to M_max tokens (the split-K
+    // slabs grow with N, so N_max bounds them); slot 1: the fused ops' rows
+    size_t need0 = 0;
+    for (int m = 2; m <= M_max; ++m) need0 = std::max(need0, plan_mmq(m, K_max, N_max, di.cus).total);
+    const size_t need1 = 2 * (size_t)M_max * N_max * sizeof(float);
+    uint8_t* p = nullptr;
+    if (need0) {
+        StreamScratch::Lease l(stream_scratch(dev, st, 0));
+        const int rc = l.get(need0, st, &p);
+        if (rc != FQ_OK) return rc;
+    }
+    if (need1) {
+        StreamScratch::Lease l(stream_scratch(dev, st, 1));
+        const int rc = l.get(need1, st, &p);
+        if (rc != FQ_OK) return rc;
+    }
+    return FQ_OK;
+}
+
+int fq_release_workspace(void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    e = hipStreamSynchronize(st);  // queued work may still read the buffers
+    if (e != hipSuccess) return hip_fail(e);
+    for (int slot = 0; slot < 2; ++slot) {
+        StreamScratch& s = stream_scratch(dev, st, slot);
+        std::lock_guard<std::mutex> lk(s.mu);
+        for (uint8_t* r : s.retired) hipFree(r);
+        s.retired.clear();
+        if (s.p) hipFree(s.p);
+        s.p = nullptr;
+        s.n = 0;
+    }
+    return FQ_OK;
 }
 
 }  // extern "C"

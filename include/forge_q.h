@@ -25,9 +25,14 @@
  *  - Return value: FQ_OK or one of the FQ_ERR_* codes below; the reference
  *    throws std::runtime_error for the same conditions (matmul.cpp:1135-1146,
  *    1163-1165, 1315) or launches unchecked.
- *  - Calls that need a split-K partial buffer use a library-owned per-device,
- *    per-stream workspace that grows on demand and lives until the process
- *    ends; concurrent calls on one stream are ordered by the stream.
+ *  - Calls on the M > 1 matrix-core path and the GGUF fused ops use a
+ *    library-owned per-device, per-stream workspace (token operands, split-K
+ *    partial slabs, intermediate rows).  It grows on demand inside a call
+ *    (hipMalloc, no host synchronisation; a superseded buffer is kept until
+ *    fq_release_workspace) and lives until the process ends.  Under HIP-graph
+ *    capture a call that would have to grow it returns FQ_ERR_WORKSPACE:
+ *    size it first with fq_reserve_workspace.  The matmul.cpp:31-54
+ *    thread-local grow-only buffer of the reference plays the same role.
  */
 #ifndef FORGE_Q_H
 #define FORGE_Q_H
@@ -45,6 +50,7 @@ extern "C" {
 #define FQ_ERR_HIP 4      /* the HIP runtime reported an error (fq_last_hip_error) */
 #define FQ_ERR_NO_DEVICE 5
 #define FQ_ERR_ALIGN 6     /* a packed-layout pointer is not 16-byte aligned       */
+#define FQ_ERR_WORKSPACE 7 /* the workspace would have to grow during graph capture */
 
 /* DataType values accepted by the entry points. */
 #define FQ_DTYPE_Q4_0 2u
@@ -191,6 +197,19 @@ int fq_ffn_down_residual(uint32_t dtype, const float* x, const void* w, const fl
 /* M = 1 over packed weights. */
 int fq_ffn_down_residual_packed(uint32_t dtype, const float* x, const void* w_packed,
                                 const float* residual, float* y, int K, int N, void* stream);
+
+/* Sizes the calling stream's workspace (current device) for every call with
+ * at most M_max tokens, K_max columns and N_max rows, so that later calls
+ * allocate nothing and can be captured into a HIP graph.  Replaces the
+ * reference's grow-on-first-use scratch (src/operators/cpu/matmul.cpp:31-54,
+ * the thread-local buffer behind the CUDA Q8_0 M > 32 path), which has no
+ * reserve call of its own. */
+int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream);
+
+/* Synchronises the stream and frees its workspace (current device), including
+ * buffers superseded by growth.  No counterpart in the reference (its scratch
+ * lives until the thread ends). */
+int fq_release_workspace(void* stream);
 
 #ifdef __cplusplus
 }

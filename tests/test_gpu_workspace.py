@@ -1,0 +1,70 @@
+"""The per-stream workspace of the M > 1 matrix-core path: reserved up front
+it lets a call be captured into a HIP graph (every replay matches the eager
+result); during capture a call that would have to grow it fails with
+FQ_ERR_WORKSPACE instead of allocating."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from forge_amd import _lib, synth
+from forge_amd import formats as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _mm(L, dtype, x, w, y, M, K, N, stream):
+    return L.fq_matmul_transB(dtype, x.data_ptr(), w.data_ptr(), None, 0, 0, y.data_ptr(), M, K,
+                              N, stream)
+
+
+def test_reserved_workspace_graph_replays():
+    L = _lib.lib()
+    dtype, M, K, N = F.Q4_K, 16, 4096, 2000  # MFMA path with K-splits
+    w = torch.from_numpy(synth.make_weights(dtype, N, K, 31).reshape(-1)).cuda()
+    x = torch.from_numpy(synth.make_x(M, K, 32)).cuda()
+    side = torch.cuda.Stream()
+    y_eager = torch.empty(M, N, device="cuda")
+    y_graph = torch.empty(M, N, device="cuda")
+    with torch.cuda.stream(side):
+        assert L.fq_reserve_workspace(M, K, N, side.cuda_stream) == 0
+        assert _mm(L, dtype, x, w, y_eager, M, K, N, side.cuda_stream) == 0
+    torch.cuda.synchronize()
+    ref = y_eager.cpu().numpy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        st = _mm(L, dtype, x, w, y_graph, M, K, N, side.cuda_stream)
+    assert st == 0
+    for r in range(3):
+        y_graph.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y_graph.cpu().numpy(), ref, err_msg=f"replay {r}")
+        # eager work on the same workspace between replays
+        with torch.cuda.stream(side):
+            assert _mm(L, dtype, x * 2, w, y_eager, M, K, N, side.cuda_stream) == 0
+        torch.cuda.synchronize()
+    del g
+    assert L.fq_release_workspace(side.cuda_stream) == 0
+
+
+def test_growth_under_capture_is_refused():
+    L = _lib.lib()
+    dtype, M, K, N = F.Q8_0, 24, 2048, 1024
+    w = torch.from_numpy(synth.make_weights(dtype, N, K, 33).reshape(-1)).cuda()
+    x = torch.from_numpy(synth.make_x(M, K, 34)).cuda()
+    y = torch.empty(M, N, device="cuda")
+    side = torch.cuda.Stream()  # a fresh stream: no workspace yet
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        st = _mm(L, dtype, x, w, y, M, K, N, side.cuda_stream)
+    assert st == _lib.FQ_ERR_WORKSPACE
+    assert b"fq_reserve_workspace" in L.fq_status_str(st)
+    del g
+    # outside capture the same call grows the workspace and runs
+    with torch.cuda.stream(side):
+        assert _mm(L, dtype, x, w, y, M, K, N, side.cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert np.isfinite(y.cpu().numpy()).all()
