@@ -45,6 +45,7 @@ SIGNATURES = {
     "fq_fused_qkv_packed": (_I, [_U, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "fq_ffn_down_residual": (_I, [_U, _P, _P, _P, _P, _I, _I, _I, _P]),
     "fq_ffn_down_residual_packed": (_I, [_U, _P, _P, _P, _P, _I, _I, _P]),
+    "fq_matmul_transB_noalloc": (_I, [_U, _P, _P, _P, _I, _L, _P, _I, _I, _I, _P]),
     "fq_reserve_workspace": (_I, [_I, _I, _I, _P]),
     "fq_release_workspace": (_I, [_P]),
 }

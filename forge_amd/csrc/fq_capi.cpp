@@ -217,6 +217,32 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
                int64_t bias_len, float* y, int M, int K, int N, hipStream_t st,
                uint8_t* fixed = nullptr, size_t fixed_cap = 0);
 
+// Fixed workspace of fq_matmul_transB_noalloc, for callers that cannot
+// allocate (HIP-graph capture, serving loops that forbid hipMalloc).  Every
+// GPU the library runs on holds its own copy until the process ends.  It is
+// shared by every call of that entry point on the device: calls that overlap
+// on one GPU race on it.  Nothing in it has to start at zero (the token
+// preparation writes every operand, each K-split writes its whole slab).
+constexpr size_t kNoAllocBytes = (size_t)64 << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the host-side name is only a stand-in for the symbol).
+int noalloc_workspace(int dev, uint8_t** out) {
+    static std::mutex mu;
+    static std::map<int, uint8_t*> ptrs;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = ptrs.find(dev);
+    if (it == ptrs.end()) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e);
+        it = ptrs.emplace(dev, static_cast<uint8_t*>(p)).first;
+    }
+    *out = it->second;
+    return FQ_OK;
+}
+
 int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
                 const void* w3_packed, int n1, int n2, int mode, const float* bias,
                 int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf);
@@ -490,7 +516,8 @@ const char* fq_status_str(int status) {
         case FQ_ERR_ALIGN: return "packed buffer not 16-byte aligned";
         case FQ_ERR_WORKSPACE:
             return "workspace too small (reserve it with fq_reserve_workspace before graph "
-                   "capture)";
+                   "capture; fq_matmul_transB_noalloc: the call needs more than its fixed "
+                   "64 MiB)";
         default: return "unknown status";
     }
 }
@@ -525,6 +552,23 @@ int fq_matmul_transB(uint32_t dtype, const float* x, const void* w, const float*
     else if (bias && bias_ndim != 0) return FQ_ERR_SHAPE;
     return run_matmul(dtype, x, w, bias, mode, bias_len, y, M, K, N,
                       static_cast<hipStream_t>(stream));
+}
+
+int fq_matmul_transB_noalloc(uint32_t dtype, const float* x, const void* w, const float* bias,
+                             int bias_ndim, int64_t bias_len, float* y, int M, int K, int N,
+                             void* stream) {
+    int mode = 0;
+    if (bias && bias_ndim == 1) mode = 1;
+    else if (bias && bias_ndim == 2) mode = 2;
+    else if (bias && bias_ndim != 0) return FQ_ERR_SHAPE;
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    uint8_t* ws = nullptr;
+    const int rc = noalloc_workspace(dev, &ws);
+    if (rc != FQ_OK) return rc;
+    return run_matmul(dtype, x, w, bias, mode, bias_len, y, M, K, N,
+                      static_cast<hipStream_t>(stream), ws, kNoAllocBytes);
 }
 
 int fq_dequant_rows(uint32_t dtype, const void* w, float* out, int N, int K, void* stream) {

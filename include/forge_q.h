@@ -50,7 +50,8 @@ extern "C" {
 #define FQ_ERR_HIP 4      /* the HIP runtime reported an error (fq_last_hip_error) */
 #define FQ_ERR_NO_DEVICE 5
 #define FQ_ERR_ALIGN 6     /* a packed-layout pointer is not 16-byte aligned       */
-#define FQ_ERR_WORKSPACE 7 /* the workspace would have to grow during graph capture */
+#define FQ_ERR_WORKSPACE 7 /* the workspace would have to grow during graph capture,
+                              or a call exceeds fq_matmul_transB_noalloc's fixed one */
 
 /* DataType values accepted by the entry points. */
 #define FQ_DTYPE_Q4_0 2u
@@ -197,6 +198,20 @@ int fq_ffn_down_residual(uint32_t dtype, const float* x, const void* w, const fl
 /* M = 1 over packed weights. */
 int fq_ffn_down_residual_packed(uint32_t dtype, const float* x, const void* w_packed,
                                 const float* residual, float* y, int K, int N, void* stream);
+
+/* fq_matmul_transB without any allocation: the same results (the same
+ * kernels and launch plan), with the M > 1 matrix-core path's workspace taken
+ * from a fixed 64 MiB device array that the library holds on every GPU it
+ * runs on, instead of the per-stream workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP-graph
+ * capture, serving loops and harnesses that forbid hipMalloc).  Returns
+ * FQ_ERR_WORKSPACE when a call needs more than 64 MiB (for example M = 512 at
+ * K = 4096 needs 42 MiB with 4 K-splits over 4096 rows).  All calls on one GPU
+ * share the array: calls that overlap on one GPU (several streams or host
+ * threads) race on it and must be serialised by the caller. */
+int fq_matmul_transB_noalloc(uint32_t dtype, const float* x, const void* w, const float* bias,
+                             int bias_ndim, int64_t bias_len, float* y, int M, int K, int N,
+                             void* stream);
 
 /* Sizes the calling stream's workspace (current device) for every call with
  * at most M_max tokens, K_max columns and N_max rows, so that later calls
