@@ -61,6 +61,9 @@ def parse():
                    help="skip the per-configuration lines (configs 0-4, Q4_0 7B shapes)")
     p.add_argument("--formats", action="store_true",
                    help="also time the five formats outside the configs (stderr)")
+    p.add_argument("--shape", action="append", default=[], metavar="DTYPE:NxK[:M]",
+                   help="only time these shapes (e.g. q4_0:152064x3584:1), GGUF and, for "
+                        "M = 1, aligned layout; one JSON line each on stdout")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--layout", choices=("packed", "gguf"), default="packed",
@@ -384,6 +387,23 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+
+    if args.shape:
+        from forge_amd import formats as F
+        names = {f.name.lower(): dt for dt, f in F.FORMATS.items()}
+        for spec in args.shape:
+            parts = spec.split(":")
+            dt = names[parts[0].lower()]
+            N, K = (int(v) for v in parts[1].lower().split("x"))
+            M = int(parts[2]) if len(parts) > 2 else 1
+            w_np = synth.make_weights(dt, N, K, seed=N + K)
+            line = time_config(spec, dt, N, K, M, cpu=not args.no_cpu, w_np=w_np)
+            if M == 1 and dt in (F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K):
+                pk = time_config(spec, dt, N, K, M, packed=True, w_np=w_np)
+                line["packed_us"] = pk["us"]
+                line["packed_pct_hbm"] = pk["pct_hbm"]
+            print(json.dumps(line), flush=True)
+        return
 
     # ---- inputs: seeded blocks, two device copies of the whole step per layout
     host_w = [synth.make_weights(dt, N, K, seed=2000 + i) for i, (_, dt, N, K) in enumerate(CFG2)]

@@ -448,9 +448,11 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     // partial sums a work-group can buffer: a static 4096-entry array for the
     // packed kernel, the LDS left after the records and wave buffers for GGUF
     long pcap = 4096;
+    int nl = 1;
     const void* fn =
-        gguf ? fq::gemvg_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg)
-             : fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, mode);
+        gguf ? fq::gemvg_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl)
+             : fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl,
+                                   mode);
     if (gguf) {
         if (lds + 64 * 4 > lds_cap) return FQ_ERR_SHAPE;
         pcap = std::min<long>(4096, (long)(lds_cap - lds) / 4);
@@ -465,7 +467,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     // one work-group per resident slot, each owning a contiguous row range
     // with at least one row per wave, and whose row x K-slice partial sums fit
     // its LDS buffer (slices of 64 lane units)
-    const long ns = (units + 63) / 64;
+    const long ns = (units + 64 * nl - 1) / (64 * nl);
     long G = (long)di.cus * per_cu;
     G = std::max(1L, std::min<long>(G, ((long)NV + wpb - 1) / wpb));
     auto max_rows = [&](long g) { return dual ? 2 * ((N + g - 1) / g) : (NV + g - 1) / g; };

@@ -273,15 +273,24 @@ struct Gk<Q6_K> {  // ql[128] @0, qh[64] @128, sc[16] @192, d @208; unit u = 4 s
     }
 };
 
-// Bytes of one K-slice (64 lane units) of a GGUF row, and the dwordx4 pieces
-// per lane that cover its aligned superset (at most 14 bytes of misalignment).
-template <int F>
+// Bytes of one K-slice (64 NL lane units) of a GGUF row, and the dwordx4
+// pieces per lane that cover the aligned superset of `units` lane units (at
+// most 14 bytes of misalignment).
+template <int F, int NL>
 constexpr int slice_bytes() {
-    return 64 / Gk<F>::UPB * Gk<F>::BB;
+    return 64 * NL / Gk<F>::UPB * Gk<F>::BB;
 }
 template <int F>
 constexpr int slice_pieces(int units) {
     return ((units / Gk<F>::UPB * Gk<F>::BB + 14 + 15) / 16 + 63) / 64;
+}
+
+// Lane units per lane and step: two for the 32-weight formats on rows of more
+// than 64 units (halves the per-step reduction and bookkeeping per weight),
+// one otherwise.
+template <int F>
+constexpr int lane_units(int units) {
+    return (F == Q4_0 || F == Q4_1) && units > 64 ? 2 : 1;
 }
 
 template <int GP>
@@ -368,9 +377,9 @@ struct RegSel<F, 0> {
 };
 
 // First byte of step t's K-slice in a GGUF row.
-template <int F, int MODE>
+template <int F, int NL, int MODE>
 __device__ __forceinline__ const uint8_t* gslice(const GemvArgs& a, const It& t, int lo) {
-    return row_ptr<MODE>(a, min(lo + t.r, a.N - 1)) + (size_t)t.s * slice_bytes<F>();
+    return row_ptr<MODE>(a, min(lo + t.r, a.N - 1)) + (size_t)t.s * slice_bytes<F, NL>();
 }
 
 template <int F, int NL, int MODE, int GP>
@@ -383,13 +392,12 @@ __device__ __forceinline__ void pload(typename RegSel<F, GP>::T (&f)[NL], const 
         for (int c = 0; c < NL; ++c)
             f[c] = Pk<F>::load(r, min(v0 + lane + 64 * c, a.U - 1), a.U);
     } else {
-        static_assert(NL == 1, "GGUF slices are 64 lane units");
         // pointer arithmetic (not integer casts) keeps the global address
         // space, so these stay global_load (vmcnt only)
-        const uint8_t* g0 = gslice<F, MODE>(a, t, lo);
+        const uint8_t* g0 = gslice<F, NL, MODE>(a, t, lo);
         const int shift = (int)(reinterpret_cast<uintptr_t>(g0) & 15);
         const uint8_t* a0 = g0 - shift;
-        const int units = min(64, a.U - 64 * t.s);
+        const int units = min(64 * NL, a.U - 64 * NL * t.s);
         const int n16 = (shift + units / Gk<F>::UPB * Gk<F>::BB + 15) >> 4;
 #pragma unroll
         for (int i = 0; i < GP; ++i) f[0].v[i] = ldg128<true>(a0 + 16 * min(lane + 64 * i, n16 - 1));
@@ -445,12 +453,19 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], It& cp
     } else {
 #pragma unroll
         for (int i = 0; i < GP; ++i) reinterpret_cast<uint4*>(wbuf)[lane + 64 * i] = f[0].v[i];
-        const int shift = (int)(reinterpret_cast<uintptr_t>(gslice<F, MODE>(a, cp, lo)) & 15);
-        const int v = v0 + lane;
-        const auto raw = Gk<F>::read(wbuf + shift, min(v, a.U - 1) - v0);
+        const int shift =
+            (int)(reinterpret_cast<uintptr_t>(gslice<F, NL, MODE>(a, cp, lo)) & 15);
+        typename Pk<F>::Raw raw[NL];
+#pragma unroll
+        for (int c = 0; c < NL; ++c)
+            raw[c] = Gk<F>::read(wbuf + shift, min(v0 + lane + 64 * c, a.U - 1) - v0);
         pload<F, NL, MODE, GP>(f, a, ld, lo, lane);
-        const float t = Pk<F>::dot(raw, min(v, a.U - 1), L[0]);
-        acc = v < a.U ? t : 0.0f;
+#pragma unroll
+        for (int c = 0; c < NL; ++c) {
+            const int v = v0 + lane + 64 * c;
+            const float t = Pk<F>::dot(raw[c], min(v, a.U - 1), L[c]);
+            acc += v < a.U ? t : 0.0f;
+        }
     }
     const float s = __builtin_bit_cast(
         float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
@@ -565,15 +580,28 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
 constexpr int WGP = 1024;
 constexpr int DP = 3;
 
+// Two lane units per lane hold both units' activation limbs in registers:
+// more than the 128 VGPRs of a 1024-thread work-group, so they run 512.
+template <int NL>
+constexpr int depth() {
+    return DP;
+}
+template <int NL, int WG>
+constexpr int nl_wg() {
+    return NL == 2 ? 512 : WG;
+}
+
 template <int F, int NL>
 const void* pfn2(bool bias) {
-    return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, true, WGP>)
-                : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, false, WGP>);
+    constexpr int WG = nl_wg<NL, WGP>();
+    return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, depth<NL>(), true, WG>)
+                : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, depth<NL>(), false, WG>);
 }
 
 template <int F>
-const void* pfn(bool bias) {
-    return pfn2<F, 1>(bias);
+const void* pfn(int units, bool bias, int* nl) {
+    *nl = lane_units<F>(units);
+    return *nl == 2 ? pfn2<F, 2>(bias) : pfn2<F, 1>(bias);
 }
 
 template <int F>
@@ -596,25 +624,35 @@ constexpr int gwg() {
     return GP >= 4 ? 512 : WGP;
 }
 
-template <int F, int GP>
+template <int F, int NL, int GP>
 const void* gfn2(bool bias) {
-    if constexpr (GP > max_pieces<F>()) {
+    if constexpr (GP > max_pieces<F>() * NL) {
         return nullptr;
     } else {
-        constexpr int WG = gwg<GP>();
-        return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, true, WG, ONE, GP>)
-                    : reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WG, ONE, GP>);
+        constexpr int WG = nl_wg<NL, gwg<GP>()>();
+        return bias
+                   ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, depth<NL>(), true, WG, ONE, GP>)
+                   : reinterpret_cast<const void*>(
+                         &gemvp_kernel<F, NL, depth<NL>(), false, WG, ONE, GP>);
     }
 }
 
 template <int F>
-const void* gfn(int units, bool bias, int* gp) {
-    *gp = slice_pieces<F>(units < 64 ? units : 64);
+const void* gfn(int units, bool bias, int* gp, int* nl) {
+    *nl = lane_units<F>(units);
+    *gp = slice_pieces<F>(units < 64 * *nl ? units : 64 * *nl);
+    if (*nl == 2) {
+        switch (*gp) {
+            case 2: return gfn2<F, 2, 2>(bias);
+            case 3: return gfn2<F, 2, 3>(bias);
+            default: return nullptr;
+        }
+    }
     switch (*gp) {
-        case 1: return gfn2<F, 1>(bias);
-        case 2: return gfn2<F, 2>(bias);
-        case 3: return gfn2<F, 3>(bias);
-        case 4: return gfn2<F, 4>(bias);
+        case 1: return gfn2<F, 1, 1>(bias);
+        case 2: return gfn2<F, 1, 2>(bias);
+        case 3: return gfn2<F, 1, 3>(bias);
+        case 4: return gfn2<F, 1, 4>(bias);
         default: return nullptr;
     }
 }
@@ -632,21 +670,23 @@ void gemvp_geometry(int dtype, int K, int* units, int* records) {
     }
 }
 
-// Kernel for a row of `units` lane units: K-slices of 64 units (one per lane).
-// mode 1: the fused gate/up form, 2: the fused QKV form (bias unused in both).
+// Kernel for a row of `units` lane units: K-slices of 64 nl units (nl per
+// lane).  mode 1: the fused gate/up form, 2: the fused QKV form (bias unused
+// in both).
 const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg,
-                            int mode) {
-    (void)units;
+                            int* nl, int mode) {
     const void* fn = nullptr;
+    *nl = 1;
     switch (dtype) {
-        case Q4_0: fn = mode ? pfn_mode<Q4_0>(mode) : pfn<Q4_0>(bias); break;
-        case Q4_1: fn = mode ? pfn_mode<Q4_1>(mode) : pfn<Q4_1>(bias); break;
-        case Q8_0: fn = mode ? pfn_mode<Q8_0>(mode) : pfn<Q8_0>(bias); break;
-        case Q4_K: fn = mode ? pfn_mode<Q4_K>(mode) : pfn<Q4_K>(bias); break;
-        case Q6_K: fn = mode ? pfn_mode<Q6_K>(mode) : pfn<Q6_K>(bias); break;
+        case Q4_0: fn = mode ? pfn_mode<Q4_0>(mode) : pfn<Q4_0>(units, bias, nl); break;
+        case Q4_1: fn = mode ? pfn_mode<Q4_1>(mode) : pfn<Q4_1>(units, bias, nl); break;
+        case Q8_0: fn = mode ? pfn_mode<Q8_0>(mode) : pfn<Q8_0>(units, bias, nl); break;
+        case Q4_K: fn = mode ? pfn_mode<Q4_K>(mode) : pfn<Q4_K>(units, bias, nl); break;
+        case Q6_K: fn = mode ? pfn_mode<Q6_K>(mode) : pfn<Q6_K>(units, bias, nl); break;
     }
+    if (mode) *nl = 1;
     *lds = (size_t)records * RECB;
-    *wg = WGP;
+    *wg = *nl == 2 ? nl_wg<2, WGP>() : WGP;
     return fn;
 }
 
@@ -654,17 +694,18 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
 // buffer).  *lds_fixed: the records and the wave buffers; the host adds the
 // partial-sum buffer after them.
 const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
-                            int* wg) {
+                            int* wg, int* nl) {
     int gp = 0;
     const void* fn = nullptr;
+    *nl = 1;
     switch (dtype) {
-        case Q4_0: fn = gfn<Q4_0>(units, bias, &gp); break;
-        case Q4_1: fn = gfn<Q4_1>(units, bias, &gp); break;
-        case Q8_0: fn = gfn<Q8_0>(units, bias, &gp); break;
-        case Q4_K: fn = gfn<Q4_K>(units, bias, &gp); break;
-        case Q6_K: fn = gfn<Q6_K>(units, bias, &gp); break;
+        case Q4_0: fn = gfn<Q4_0>(units, bias, &gp, nl); break;
+        case Q4_1: fn = gfn<Q4_1>(units, bias, &gp, nl); break;
+        case Q8_0: fn = gfn<Q8_0>(units, bias, &gp, nl); break;
+        case Q4_K: fn = gfn<Q4_K>(units, bias, &gp, nl); break;
+        case Q6_K: fn = gfn<Q6_K>(units, bias, &gp, nl); break;
     }
-    *wg = gp >= 4 ? gwg<4>() : WGP;
+    *wg = *nl == 2 ? nl_wg<2, WGP>() : gp >= 4 ? gwg<4>() : WGP;
     *lds_fixed = (size_t)records * RECB + (size_t)(*wg / 64) * gp * 1024;
     return fn;
 }

@@ -36,12 +36,13 @@ hipError_t launch_raw(const void* fn, const GemvArgs& a, int grid, int wg, size_
                       hipStream_t st);
 // packed-layout batch-1 kernels (fq_gemvp.hip)
 void gemvp_geometry(int dtype, int K, int* units, int* records);
+// nl: lane units per lane and step (K-slices are 64 nl units)
 const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg,
-                            int mode = 0);
+                            int* nl, int mode = 0);
 // the same kernel over GGUF rows; *lds_fixed excludes the partial-sum buffer
 // (4 bytes per row x K-slice of a work-group, placed after it)
 const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
-                            int* wg);
+                            int* wg, int* nl);
 hipError_t launch_pack(int dtype, const uint8_t* src, uint8_t* dst, int N, int K, bool pack,
                        int grid, hipStream_t st);
 hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st);
