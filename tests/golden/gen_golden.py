@@ -6,7 +6,11 @@ inputs and stores inputs and outputs as small .npz fixtures beside this
 script.  The fixtures are data: block bytes, activations, the reference's
 dequantized rows and the reference's ops::matmul_transB outputs.
 
-Usage:  python tests/golden/gen_golden.py [format ...]   (default: all)
+Usage:  python tests/golden/gen_golden.py [format ... | fused]   (default: all)
+
+``fused`` writes golden_fused.npz: the reference's fused decode operators
+(ffn_up_fused, the fused QKV, gate+up and down+residual CPU kernels) on
+seeded inputs.
 """
 from __future__ import annotations
 
@@ -89,8 +93,94 @@ def extreme_payload(w, f, K):
         blk[3::4, :, lo:hi] = 0x7F
 
 
+def _in_silu_range(dt, x, wg, K):
+    """x scaled by a power of two so that every gate value stays within
+    |g| <= 32.  The reference's AVX2 silu_multiply (elementwise.cpp:100-160)
+    builds exp(-g) from a 2^n exponent without clamping n, so for |g| above
+    about 87 it returns garbage (e.g. silu(-129) * u = -3.3e4); the synthetic
+    K-quant weights give gate values in the hundreds at x ~ N(0, 1)."""
+    d = np.zeros((wg.shape[0], K), np.float32)
+    assert lib().fqr_dequant_rows(dt, wg.ctypes.data_as(P), d.ctypes.data_as(P),
+                                  wg.shape[0], K) == 0
+    gmax = float(np.max(np.abs(x.astype(np.float64) @ d.T.astype(np.float64))))
+    k = 0
+    while gmax / 2.0 ** k > 32.0:
+        k += 1
+    return np.ascontiguousarray((x * np.float32(2.0 ** -k)).astype(np.float32))
+
+
+def fused_goldens(L):
+    """The reference's fused operators (its own compiled CPU code) on small
+    seeded inputs: weights under "<op>/<fmt>/<w...>", per token count
+    "<op>/<fmt>/M<m>/{x,r,y}"."""
+    out = {}
+
+    def arr(a):
+        return np.ascontiguousarray(a)
+
+    for dt in (F.Q4_0, F.Q4_K, F.Q6_K, F.Q8_0):
+        f = F.fmt(dt)
+        K = 512
+        N = 21
+        wg = synth.make_weights(dt, N, K, seed=900 + dt)
+        wu = synth.make_weights(dt, N, K, seed=950 + dt)
+        for M in (1, 3):
+            x = _in_silu_range(dt, synth.make_x(M, K, seed=1000 + 10 * dt + M), wg, K)
+            y = np.zeros((M, N), np.float32)
+            assert L.fqr_ffn_up_fused(dt, arr(x).ctypes.data_as(P), wg.ctypes.data_as(P),
+                                      wu.ctypes.data_as(P), y.ctypes.data_as(P), M, K, N, 4) == 0
+            key = f"ffn_up_fused/{f.name}"
+            out.update({f"{key}/M{M}/x": x, f"{key}/wg": wg, f"{key}/wu": wu,
+                        f"{key}/M{M}/y": y, f"{key}/dtype": np.int64(dt)})
+    for dt in (F.Q4_0, F.Q4_K):
+        f = F.fmt(dt)
+        K = 512
+        Nq, Nk, Nv = 36, 12, 12
+        wq = synth.make_weights(dt, Nq, K, seed=1100 + dt)
+        wk = synth.make_weights(dt, Nk, K, seed=1150 + dt)
+        wv = synth.make_weights(dt, Nv, K, seed=1175 + dt)
+        wg = synth.make_weights(dt, 22, K, seed=1200 + dt)
+        wu = synth.make_weights(dt, 22, K, seed=1250 + dt)
+        for M in (1, 2):
+            x = _in_silu_range(dt, synth.make_x(M, K, seed=1300 + 10 * dt + M), wg, K)
+            y = np.zeros((M, Nq + Nk + Nv), np.float32)
+            assert L.fqr_fused_qkv(dt, arr(x).ctypes.data_as(P), wq.ctypes.data_as(P),
+                                   wk.ctypes.data_as(P), wv.ctypes.data_as(P),
+                                   y.ctypes.data_as(P), M, K, Nq, Nk, Nv, 4) == 0
+            key = f"fused_qkv/{f.name}"
+            out.update({f"{key}/M{M}/x": x, f"{key}/wq": wq, f"{key}/wk": wk, f"{key}/wv": wv,
+                        f"{key}/M{M}/y": y, f"{key}/dtype": np.int64(dt)})
+            y = np.zeros((M, 22), np.float32)
+            assert L.fqr_fused_ffn_up(dt, arr(x).ctypes.data_as(P), wg.ctypes.data_as(P),
+                                      wu.ctypes.data_as(P), y.ctypes.data_as(P), M, K, 22, 4) == 0
+            key = f"fused_ffn_up/{f.name}"
+            out.update({f"{key}/M{M}/x": x, f"{key}/wg": wg, f"{key}/wu": wu,
+                        f"{key}/M{M}/y": y, f"{key}/dtype": np.int64(dt)})
+    for dt in (F.Q4_0, F.Q6_K):
+        f = F.fmt(dt)
+        K = 512
+        N = 24
+        w = synth.make_weights(dt, N, K, seed=1400 + dt)
+        for M in (1, 2):
+            x = synth.make_x(M, K, seed=1500 + 10 * dt + M)
+            r = synth.make_x(M, N, seed=1600 + 10 * dt + M)
+            y = np.zeros((M, N), np.float32)
+            assert L.fqr_fused_down_residual(dt, arr(x).ctypes.data_as(P), w.ctypes.data_as(P),
+                                             arr(r).ctypes.data_as(P), y.ctypes.data_as(P), M, K,
+                                             N, 4) == 0
+            key = f"fused_down_residual/{f.name}"
+            out.update({f"{key}/M{M}/x": x, f"{key}/w": w, f"{key}/M{M}/r": r,
+                        f"{key}/M{M}/y": y, f"{key}/dtype": np.int64(dt)})
+    path = os.path.join(HERE, "golden_fused.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} B)")
+
+
 def main():
     L = lib()
+    if sys.argv[1:] == ["fused"]:
+        fused_goldens(L)
+        return
     only = {F.fmt(a).dtype for a in sys.argv[1:]}
     for dt, f in F.FORMATS.items():
         if only and dt not in only:

@@ -1,11 +1,15 @@
 """GPU parity of the fused decode ops: FFN up-projection silu(x Wg^T) * (x Wu^T),
 QKV projection [x Wq^T | x Wk^T | x Wv^T] and down-projection + residual.
 
-Mirrors ops::ffn_up_fused (reference matmul.cpp:1472-1533).  The oracle is
-the exact product: the fp64 matmuls over the bit-exact dequantized weights,
-then silu(g) * u in fp64.  Bar: relative L2 <= 1e-5 and max abs error <=
-1e-4 * max |y| (the fused op's output is a product of two matmul outputs, so
-the matmul max-abs bound is restated relative to the output scale).
+Mirrors ops::ffn_up_fused (reference matmul.cpp:1472-1533) and the fused
+operators of operator_matmul.h:10-48.  Two checks:
+  * against the exact product: the fp64 matmuls over the bit-exact dequantized
+    weights, then silu(g) * u in fp64;
+  * against the reference's own fused CPU operators on the committed goldens
+    (tests/golden/golden_fused.npz, written by tests/golden/gen_golden.py).
+Bar (helpers.assert_close_silu_mul): relative L2 <= 1e-5, and the matmul
+max-abs bar 1e-3 ||x||_2 max|W| carried through silu(g) * u to first order.
+QKV and down+residual outputs are matmul outputs and use the matmul bar.
 """
 from __future__ import annotations
 
@@ -16,24 +20,23 @@ import torch
 import oracle
 from forge_amd import formats as F
 from forge_amd import ops, synth
-from helpers import REL_L2
+from helpers import GOLDEN, assert_close, assert_close_silu_mul
 from test_gpu_parity import ALL, dev_weight
 
 pytestmark = pytest.mark.gpu
 
 
-def reference(dtype, x, wg, wu, N, K):
-    g = oracle.matmul_f64(dtype, x, wg, N, K)
-    u = oracle.matmul_f64(dtype, x, wu, N, K)
-    return g * 0.5 * (1.0 + np.tanh(0.5 * g)) * u  # silu(g) * u, no overflow
+def exact_gu(dtype, x, wg, wu, N, K):
+    return oracle.matmul_f64(dtype, x, wg, N, K), oracle.matmul_f64(dtype, x, wu, N, K)
 
 
-def check(y, ref, what):
-    y = np.asarray(y, np.float64).reshape(ref.shape)
-    rel = np.linalg.norm(y - ref) / max(np.linalg.norm(ref), 1e-30)
-    assert rel <= REL_L2, f"{what}: rel-L2 {rel:.3e}"
-    mx = np.max(np.abs(y - ref))
-    assert mx <= 1e-4 * np.max(np.abs(ref)), f"{what}: max abs {mx:.3e}"
+def wmax(dtype, ws, K):
+    return max(float(np.max(np.abs(oracle.dequant(dtype, w, w.shape[0], K)))) for w in ws)
+
+
+def check(y, dtype, x, wg, wu, N, K, what):
+    g, u = exact_gu(dtype, x, wg, wu, N, K)
+    assert_close_silu_mul(y, g, u, x, wmax(dtype, (wg[:4096], wu[:4096]), K), what)
 
 
 def make(dtype, N, K, seed):
@@ -48,7 +51,7 @@ def test_fused_gguf(dtype, M):
     x = synth.make_x(M, K, seed=M)
     y = ops.ffn_up_fused(torch.from_numpy(x).cuda(), dev_weight(dtype, wg, N, K),
                          dev_weight(dtype, wu, N, K))
-    check(y.cpu().numpy(), reference(dtype, x, wg, wu, N, K), f"{F.fmt(dtype).name} M={M}")
+    check(y.cpu().numpy(), dtype, x, wg, wu, N, K, f"{F.fmt(dtype).name} M={M}")
 
 
 @pytest.mark.parametrize("name,dtype,N,K", [
@@ -66,12 +69,12 @@ def test_fused_packed(name, dtype, N, K):
     Pg, Pu = ops.pack_weights(Wg), ops.pack_weights(Wu)
     xd = torch.from_numpy(x).cuda()
     y = ops.ffn_up_fused_packed(xd, Pg, Pu)
-    ref = reference(dtype, x, wg, wu, N, K).reshape(-1)
-    check(y.cpu().numpy(), ref, name)
+    check(y.cpu().numpy(), dtype, x, wg, wu, N, K, name)
     # the same numbers as the unfused packed GEMVs and a SiLU-multiply
-    g = ops.gemv_packed(xd, Pg).double()
-    u = ops.gemv_packed(xd, Pu).double()
-    check(y.cpu().numpy(), (torch.nn.functional.silu(g) * u).cpu().numpy(), name + " vs unfused")
+    g = ops.gemv_packed(xd, Pg).double().cpu().numpy().reshape(1, -1)
+    u = ops.gemv_packed(xd, Pu).double().cpu().numpy().reshape(1, -1)
+    assert_close_silu_mul(y.cpu().numpy(), g, u, x, wmax(dtype, (wg[:4096], wu[:4096]), K),
+                          name + " vs unfused")
     y2 = ops.ffn_up_fused_packed(xd, Pg, Pu)
     assert torch.equal(y, y2), "fused packed GEMV is not deterministic"
 
@@ -92,7 +95,6 @@ def test_fused_errors():
 
 
 def assert_matmul(y, ref, x, w_blocks_list, dtype, K, what):
-    from helpers import assert_close
     deq = np.concatenate([oracle.dequant(dtype, wb, wb.shape[0], K) for wb in w_blocks_list])
     assert_close(y, ref, x, np.array([float(np.max(np.abs(deq)))]), what)
 
@@ -145,3 +147,85 @@ def test_ffn_down_residual(dtype, M):
         yp = ops.ffn_down_residual_packed(torch.from_numpy(x).cuda(), ops.pack_weights(W),
                                           torch.from_numpy(r).cuda())
         assert_matmul(yp.cpu().numpy().reshape(1, -1), ref, x, [w], dtype, K, "packed")
+
+
+# ----------------------------------------------- the reference's fused goldens
+def _golden():
+    z = np.load(f"{GOLDEN}/golden_fused.npz", allow_pickle=False)
+    return {k: z[k] for k in z.files}
+
+
+def _cases(z, op):
+    fmts = sorted({k.split("/")[1] for k in z if k.startswith(op + "/")})
+    for f in fmts:
+        for M in sorted({int(k.split("/")[2][1:]) for k in z
+                         if k.startswith(f"{op}/{f}/M")}):
+            yield f, M
+
+
+GZ = _golden()
+
+
+@pytest.mark.parametrize("fmt,M", list(_cases(GZ, "ffn_up_fused")) + [
+    ("fused:" + f, M) for f, M in _cases(GZ, "fused_ffn_up")])
+def test_ffn_up_matches_reference_goldens(fmt, M):
+    op = "fused_ffn_up" if fmt.startswith("fused:") else "ffn_up_fused"
+    f = fmt.split(":")[-1]
+    z = GZ
+    dtype = int(z[f"{op}/{f}/dtype"])
+    wg, wu = z[f"{op}/{f}/wg"], z[f"{op}/{f}/wu"]
+    x, y_ref = z[f"{op}/{f}/M{M}/x"], z[f"{op}/{f}/M{M}/y"]
+    N, K = wg.shape[0], x.shape[1]
+    xd = torch.from_numpy(x).cuda()
+    Wg, Wu = dev_weight(dtype, wg, N, K), dev_weight(dtype, wu, N, K)
+    g, u = exact_gu(dtype, x, wg, wu, N, K)
+    wm = wmax(dtype, (wg, wu), K)
+    ys = {"gguf": ops.ffn_up_fused(xd, Wg, Wu).cpu().numpy()}
+    if M == 1 and ops.packed_row_bytes(dtype, K):
+        ys["packed"] = ops.ffn_up_fused_packed(xd, ops.pack_weights(Wg),
+                                               ops.pack_weights(Wu)).cpu().numpy()
+    for lay, y in ys.items():
+        what = f"{op} {f} M={M} {lay}"
+        assert_close_silu_mul(y, g, u, x, wm, what + " vs reference", y_ref=y_ref)
+        assert_close_silu_mul(y, g, u, x, wm, what + " vs exact")
+
+
+@pytest.mark.parametrize("fmt,M", list(_cases(GZ, "fused_qkv")))
+def test_fused_qkv_matches_reference_goldens(fmt, M):
+    z = GZ
+    key = f"fused_qkv/{fmt}"
+    dtype = int(z[f"{key}/dtype"])
+    ws = [z[f"{key}/w{c}"] for c in "qkv"]
+    x, y_ref = z[f"{key}/M{M}/x"], z[f"{key}/M{M}/y"]
+    K = x.shape[1]
+    ns = [w.shape[0] for w in ws]
+    Ws = [dev_weight(dtype, w, n, K) for w, n in zip(ws, ns)]
+    xd = torch.from_numpy(x).cuda()
+    exact = np.concatenate([oracle.matmul_f64(dtype, x, w, n, K) for w, n in zip(ws, ns)], axis=1)
+    ys = {"gguf": ops.fused_qkv(xd, *Ws).cpu().numpy()}
+    if M == 1 and ops.packed_row_bytes(dtype, K):
+        ys["packed"] = ops.fused_qkv_packed(xd, *(ops.pack_weights(W) for W in Ws)).cpu().numpy()
+    for lay, y in ys.items():
+        y = y.reshape(M, -1)
+        assert_matmul(y, y_ref, x, ws, dtype, K, f"qkv {fmt} M={M} {lay} vs reference")
+        assert_matmul(y, exact, x, ws, dtype, K, f"qkv {fmt} M={M} {lay} vs exact")
+
+
+@pytest.mark.parametrize("fmt,M", list(_cases(GZ, "fused_down_residual")))
+def test_down_residual_matches_reference_goldens(fmt, M):
+    z = GZ
+    key = f"fused_down_residual/{fmt}"
+    dtype = int(z[f"{key}/dtype"])
+    w = z[f"{key}/w"]
+    x, r, y_ref = z[f"{key}/M{M}/x"], z[f"{key}/M{M}/r"], z[f"{key}/M{M}/y"]
+    N, K = w.shape[0], x.shape[1]
+    W = dev_weight(dtype, w, N, K)
+    xd, rd = torch.from_numpy(x).cuda(), torch.from_numpy(r).cuda()
+    exact = oracle.matmul_f64(dtype, x, w, N, K) + r
+    ys = {"gguf": ops.ffn_down_residual(xd, W, rd).cpu().numpy()}
+    if M == 1:
+        ys["packed"] = ops.ffn_down_residual_packed(xd, ops.pack_weights(W), rd).cpu().numpy()
+    for lay, y in ys.items():
+        y = y.reshape(M, -1)
+        assert_matmul(y, y_ref, x, [w], dtype, K, f"down+res {fmt} M={M} {lay} vs reference")
+        assert_matmul(y, exact, x, [w], dtype, K, f"down+res {fmt} M={M} {lay} vs exact")

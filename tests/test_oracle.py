@@ -11,6 +11,7 @@ Each oracle function is checked against something it does not restate:
 from __future__ import annotations
 
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -297,3 +298,62 @@ def test_synth_distributions():
     a = synth.make_weights(F.Q4_K, 4, 512, seed=3)
     b = synth.make_weights(F.Q4_K, 4, 512, seed=3)
     assert np.array_equal(a, b)
+
+
+def test_fused_goldens_against_exact_products():
+    """golden_fused.npz holds the reference's fused CPU operators
+    (ffn_up_fused, fused QKV / gate+up / down+residual); each output agrees
+    with the exact product from the oracle's fp64 matmul at the path's bar:
+    the fixture is consistent and pins what the fused GPU ops must match."""
+    from helpers import GOLDEN, assert_close, assert_close_silu_mul
+    z = np.load(os.path.join(GOLDEN, "golden_fused.npz"), allow_pickle=False)
+    keys = set(z.files)
+    seen = 0
+    for k in sorted(keys):
+        if not k.endswith("/y"):
+            continue
+        op, f, m = k.split("/")[:3]
+        base = f"{op}/{f}"
+        dt = int(z[f"{base}/dtype"])
+        x, y = z[f"{base}/{m}/x"], z[k]
+        K = x.shape[1]
+
+        def deq_max(*ws):
+            return max(float(np.max(np.abs(oracle.dequant(dt, w, w.shape[0], K)))) for w in ws)
+
+        if op in ("ffn_up_fused", "fused_ffn_up"):
+            wg, wu = z[f"{base}/wg"], z[f"{base}/wu"]
+            g = oracle.matmul_f64(dt, x, wg, wg.shape[0], K)
+            u = oracle.matmul_f64(dt, x, wu, wu.shape[0], K)
+            assert_close_silu_mul(y, g, u, x, deq_max(wg, wu), k)
+        elif op == "fused_qkv":
+            ws = [z[f"{base}/w{c}"] for c in "qkv"]
+            ref = np.concatenate([oracle.matmul_f64(dt, x, w, w.shape[0], K) for w in ws], axis=1)
+            assert_close(y, ref, x, np.array([deq_max(*ws)]), k)
+        else:
+            w, r = z[f"{base}/w"], z[f"{base}/{m}/r"]
+            ref = oracle.matmul_f64(dt, x, w, w.shape[0], K) + r
+            assert_close(y, ref, x, np.array([deq_max(w)]), k)
+        seen += 1
+    assert seen == 20
+
+
+@pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built")
+def test_reference_silu_multiply_range():
+    """A reference behaviour the fused goldens avoid: the reference's AVX2
+    silu_multiply (elementwise.cpp:100-160) forms exp(-g) from a 2^n exponent
+    it never clamps, so for |g| beyond about 87 its result is garbage, while
+    for moderate g it is accurate.  (The GPU path computes silu exactly.)"""
+    L = oracle.load_ref()
+    K, N = 256, 8
+    w = synth.make_weights(F.Q8_0, N, K, seed=5)
+    deq = oracle.dequant(F.Q8_0, w, N, K).astype(np.float64)
+    for scale, ok in ((1e-2, True), (1e3, False)):
+        x = (synth.make_x(1, K, 6) * np.float32(scale)).astype(np.float32)
+        y = np.zeros((1, N), np.float32)
+        assert L.fqr_ffn_up_fused(F.Q8_0, oracle._p(x), oracle._p(w), oracle._p(w),
+                                  oracle._p(y), 1, K, N, 1) == 0
+        g = x.astype(np.float64) @ deq.T
+        exact = g * 0.5 * (1.0 + np.tanh(0.5 * g)) * g
+        close = np.allclose(y, exact, rtol=1e-4, atol=1e-6 * np.max(np.abs(exact)))
+        assert close == ok, (scale, float(np.max(np.abs(g))))
