@@ -22,7 +22,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 SOURCES = ["fq_dequant.hip", "fq_gemv1.hip", "fq_gemvp.hip", "fq_pack.hip", "fq_mmq.hip",
-           "fq_mmqi.hip",
+           "fq_mmqi.hip", "fq_mmqs.hip",
            "fq_capi.cpp"]
 
 COMMON = [

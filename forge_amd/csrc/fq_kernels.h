@@ -75,6 +75,12 @@ hipError_t launch_xprep(int dtype, const float* x, int M, int K, int NC, _Float1
                         float* xsum, int* ex, hipStream_t st);
 hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, int splits,
                       hipStream_t st);
+// 2..16 tokens on the fp16 matrix cores, weights streamed once (fq_mmqs.hip):
+// the token operands of launch_xprep (one token tile), bands of rows_per_wg
+// rows (at most 16 mmqs_max_tiles()) per work-group
+bool mmqs_supported(int dtype);
+int mmqs_max_tiles();
+hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hipStream_t st);
 hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,
                           int row_bytes, int grid, hipStream_t st);
 

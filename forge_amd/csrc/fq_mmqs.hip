@@ -1,0 +1,296 @@
+// fq_mmqs.hip -- small-batch (M <= 16 tokens) matmul on the fp16 matrix
+// cores, streaming the GGUF rows once.
+//
+// A work-group owns a band of rows, cut into TW tiles of 16; its waves split
+// the K dimension by super-blocks (super-block s goes to wave s % W), so each
+// wave walks its super-blocks over ALL the band's tiles and every weight byte
+// is read once by one wave.  A super-block of a tile (16 rows x 144 bytes for
+// Q4_K) is fetched with 16-byte loads along the rows into the wave's LDS
+// panel (an MFMA operand gathers 16 rows per load instruction, which costs
+// the texture addresser several times a row-contiguous load), and per
+// 64-element chunk of it (tile, chunk) the wave issues
+//
+//   D_s = A_s (16 rows x 32) . B_s (32 x 16 tokens), s = the chunk's two
+//         32-element sub-blocks, as v_mfma_f32_16x16x32_f16 twice per
+//         sub-block: x_hi and x_lo accumulate into the same fp32 D_s;
+//   A_s: exact fp16 quants (lane 16 q + r: row r, elements 8 q .. 8 q + 7 in
+//        the slot order of fq_mfma16.h);
+//   B_s: the token operands of xprep_kernel (fq_mmq.hip): x of the chunk
+//        scaled by 2^-e (one exponent per token and chunk), split into fp16
+//        hi + lo (22 significant bits), in the same slot order;
+//
+// and adds  2^e (A_0 D_0 + A_1 D_1 + B_0 S_0 + B_1 S_1)  to its accumulators,
+// with (A_s, B_s) the sub-block's affine pair of the format (Q4_K: d sc and
+// -dmin m, matmul.cpp:340-377) and S_s the scaled sub-block sums of x.  The
+// token operands of a chunk are loaded once per wave (one chunk ahead) and
+// reused by every tile of the band.
+//
+// The scale coefficients of a row come from its super-block header; D's lanes
+// hold rows 4 q' .. 4 q' + 3 of token c, so the coefficients go through a
+// small per-wave LDS table: once per super-block lane (r, q) decodes the four
+// coefficients of pair q of row r, and per chunk lane (c, q') reads those of
+// rows 4 q' .. +3.
+//
+// At the end every wave's accumulators go to LDS and the work-group adds the
+// W partial sums of each output in wave order: deterministic, no atomics.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fq_formats.h"
+#include "fq_kernels.h"
+#include "fq_mfma16.h"
+
+namespace fq {
+namespace {
+
+constexpr int KC = 64;      // K elements per chunk (as xprep_kernel)
+constexpr int XOP = 2048;   // halves per (token tile, chunk)
+constexpr int XSUM = 64;    // sub-block sums per (token tile, chunk)
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int F>
+struct Band;
+
+// Q4_K: one super-block of 16 rows is a 16 x 144-byte panel.  It is loaded
+// with 16-byte pieces (piece p of the panel: row p / 9, bytes 16 (p % 9) of
+// the row's super-block: each row a contiguous 144-byte run) and written to
+// the wave's LDS panel in the same order; the MFMA operands are then read
+// from the panel.  Chunk g of the super-block = sub-block pair g: lane
+// (r, q) takes qs bytes [32 g + 8 q, +8) of row r (low nibbles: sub-block
+// 2 g, high nibbles: 2 g + 1); the row's header is the panel's first 16
+// bytes.
+template <>
+struct Band<Q4_K> {
+    static constexpr int SBK = 256, PANEL = 16 * 144, PIECES = PANEL / 16;
+    __device__ static const uint8_t* piece(const uint8_t* row0, int row_bytes, int sb, int p) {
+        const int rr = p / 9;
+        return row0 + (size_t)rr * row_bytes + 144 * sb + 16 * (p - 9 * rr);
+    }
+    __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
+        const fq_u32x2 qs =
+            *reinterpret_cast<const fq_u32x2*>(panel + 144 * r + 16 + 32 * g + 8 * q);
+        a0 = nib8(qs.x, qs.y, 0, (_Float16)1024.0f);
+        a1 = nib8(qs.x, qs.y, 4, (_Float16)1024.0f);
+    }
+    // the four coefficients of row r for pair g: d sc_2g, d sc_2g+1,
+    // -dmin m_2g, -dmin m_2g+1
+    __device__ static float4 coef4(const uint8_t* panel, int g, int r) {
+        const fq_u32x4 h = *reinterpret_cast<const fq_u32x4*>(panel + 144 * r);
+        uint32_t sa, ma, sb, mb;
+        Fmt<Q4_K>::scale_min(uint4{h.x, h.y, h.z, h.w}, g, sa, ma, sb, mb);
+        const float d = f16_hw(h.x & 0xFFFFu), dmin = f16_hw(h.x >> 16);
+        return float4{d * (float)sa, d * (float)sb, -dmin * (float)ma, -dmin * (float)mb};
+    }
+};
+
+constexpr int NPL = 3;  // 16-byte pieces per lane per panel (144 / 64, rounded up)
+
+template <int F, int TW, int WG, bool BIAS>
+__global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
+    using B = Band<F>;
+    constexpr int W = WG / 64;
+    // per wave: TW panels (one super-block of 16 rows each) and TW tiles x 4
+    // coefficients x 16 rows; then the partial sums
+    __shared__ __attribute__((aligned(16))) uint8_t panels[W][TW][B::PANEL];
+    // per wave and tile: coefficient v of pair g, row r at coef[..][g][v][r]
+    __shared__ __attribute__((aligned(16))) float coef[W][TW][4][4][16];
+    __shared__ float part[W][TW][16][16];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;  // A operand: row r, element group q
+    const int c = lane & 15;                 // D and B operands: token column c
+    const int lo = blockIdx.x * rows_per_wg;
+    const int hi = min(a.N, lo + rows_per_wg);
+    const int ntl = (hi - lo + 15) >> 4;
+    const int nsb = a.K / B::SBK;
+
+    // piece p of a tile's panel (rows clamped into the matrix)
+    const uint8_t* prow[TW];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) prow[t] = a.w + (size_t)min(lo + 16 * t, a.N - 1) * a.row_bytes;
+    int pp[NPL], rmax[TW];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) pp[i] = min(lane + 64 * i, B::PIECES - 1);
+#pragma unroll
+    for (int t = 0; t < TW; ++t) rmax[t] = a.N - 1 - min(lo + 16 * t, a.N - 1);
+
+    f32x4 acc[TW];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const fq_u32x4* xop = reinterpret_cast<const fq_u32x4*>(a.xop);
+    auto load_panels = [&](int sb, fq_u32x4 (&pv)[TW][NPL]) {
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                const int rr = min(pp[i] / 9, rmax[t]);  // rows past N repeat the last
+                const uint8_t* p = prow[t] + (size_t)rr * a.row_bytes + 144 * sb +
+                                   16 * (pp[i] - 9 * (pp[i] / 9));
+                pv[t][i] = __builtin_nontemporal_load(reinterpret_cast<const fq_u32x4*>(p));
+            }
+    };
+
+    auto load_x = [&](int ch, fq_u32x4 (&xv)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xv[i] = xop[(size_t)ch * (XOP / 8) + 64 * i + lane];
+    };
+
+    // exponent and the two sub-block sums of token c in chunk ch
+    struct Xs {
+        int e;
+        float S0, S1;
+    };
+    auto load_s = [&](int ch) {
+        return Xs{a.ex[(size_t)ch * 16 + c], a.xsum[(size_t)ch * XSUM + c],
+                  a.xsum[(size_t)ch * XSUM + 16 + c]};
+    };
+
+    // Token operands are prefetched one chunk ahead.  (Loading all four
+    // chunks of the next super-block ahead of its panel loads, so that no
+    // short L2 load queues behind a long HBM load in the in-order vector
+    // memory counter, needs about 250 VGPRs and measured slower.)
+    int sb = wave;
+    fq_u32x4 pv[TW][NPL];
+    fq_u32x4 xv[4];  // the token operands of the chunk computed next
+    Xs xs{0, 0.0f, 0.0f};
+    if (sb < nsb) {
+        load_x(4 * sb, xv);
+        xs = load_s(4 * sb);
+        load_panels(sb, pv);
+    }
+    while (sb < nsb) {  // wave-uniform
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int i = 0; i < NPL; ++i)
+                if (lane + 64 * i < B::PIECES)
+                    *reinterpret_cast<fq_u32x4*>(&panels[wave][t][16 * (lane + 64 * i)]) = pv[t][i];
+        const int nx = sb + W;
+        load_panels(min(nx, nsb - 1), pv);  // the next super-block's loads (clamped)
+        // the super-block's coefficients: lane (r, q) decodes pair q of row r
+        // (the wave's own LDS writes precede its reads: in order)
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            if (t < ntl) {
+                const float4 cv = B::coef4(panels[wave][t], q, r);
+                coef[wave][t][q][0][r] = cv.x;
+                coef[wave][t][q][1][r] = cv.y;
+                coef[wave][t][q][2][r] = cv.z;
+                coef[wave][t][q][3][r] = cv.w;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int ch = 4 * sb + g;
+            // the following chunk's token operands (the next super-block's
+            // first after the last), in flight while this chunk computes
+            fq_u32x4 xn[4];
+            const int cn = g < 3 ? ch + 1 : 4 * min(nx, nsb - 1);
+            load_x(cn, xn);
+            const Xs xsn = load_s(cn);
+            const float S0 = xs.S0, S1 = xs.S1;
+            const float p2 = __builtin_amdgcn_ldexpf(1.0f, xs.e);
+            const h8 xh0 = __builtin_bit_cast(h8, xv[0]), xl0 = __builtin_bit_cast(h8, xv[1]);
+            const h8 xh1 = __builtin_bit_cast(h8, xv[2]), xl1 = __builtin_bit_cast(h8, xv[3]);
+#pragma unroll
+            for (int t = 0; t < TW; ++t) {
+                if (t < ntl) {  // wave-uniform
+                    h8 a0, a1;
+                    B::operands(panels[wave][t], g, r, q, a0, a1);
+                    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xh0, z, 0, 0, 0);
+                    d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xl0, d0, 0, 0, 0);
+                    f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xh1, z, 0, 0, 0);
+                    d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xl1, d1, 0, 0, 0);
+                    const float4 A0 = *reinterpret_cast<const float4*>(&coef[wave][t][g][0][4 * q]);
+                    const float4 A1 = *reinterpret_cast<const float4*>(&coef[wave][t][g][1][4 * q]);
+                    const float4 B0 = *reinterpret_cast<const float4*>(&coef[wave][t][g][2][4 * q]);
+                    const float4 B1 = *reinterpret_cast<const float4*>(&coef[wave][t][g][3][4 * q]);
+                    const float a0v[4] = {A0.x, A0.y, A0.z, A0.w};
+                    const float a1v[4] = {A1.x, A1.y, A1.z, A1.w};
+                    const float b0v[4] = {B0.x, B0.y, B0.z, B0.w};
+                    const float b1v[4] = {B1.x, B1.y, B1.z, B1.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float s = a0v[i] * d0[i];
+                        s = __builtin_fmaf(a1v[i], d1[i], s);
+                        s = __builtin_fmaf(b0v[i], S0, s);
+                        s = __builtin_fmaf(b1v[i], S1, s);
+                        acc[t][i] = __builtin_fmaf(s, p2, acc[t][i]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[i] = xn[i];
+            xs = xsn;
+        }
+        sb = nx;
+    }
+    // partial sums: D lane (c, q) holds rows 4 q + i of token c
+#pragma unroll
+    for (int t = 0; t < TW; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[wave][t][4 * q + i][c] = acc[t][i];
+    __syncthreads();
+    for (int o = threadIdx.x; o < ntl * 256; o += WG) {
+        const int t = o >> 8, rr = (o >> 4) & 15, m = o & 15;
+        const int row = lo + 16 * t + rr;
+        if (m >= a.M || row >= hi) continue;
+        float v = part[0][t][rr][m];
+        for (int w = 1; w < W; ++w) v += part[w][t][rr][m];
+        if constexpr (BIAS) {
+            if (a.bias_mode == 2) v += a.bias[(size_t)m * a.N + row];
+            else v += row < a.bias_len ? a.bias[row] : 0.0f;
+        }
+        a.y[(size_t)m * a.N + row] = v;
+    }
+}
+
+template <int F, int TW, int WG>
+const void* sfn(bool bias) {
+    return bias ? reinterpret_cast<const void*>(&mmqs_kernel<F, TW, WG, true>)
+                : reinterpret_cast<const void*>(&mmqs_kernel<F, TW, WG, false>);
+}
+
+template <int F, int WG>
+const void* sfn_tw(int tw, bool bias) {
+    switch (tw) {
+        case 1: return sfn<F, 1, WG>(bias);
+        case 2: return sfn<F, 2, WG>(bias);
+    }
+    if constexpr (WG <= 512) {
+        switch (tw) {
+            case 3: return sfn<F, 3, WG>(bias);
+            case 4: return sfn<F, 4, WG>(bias);
+        }
+    }
+    return nullptr;
+}
+
+}  // namespace
+
+bool mmqs_supported(int dtype) { return dtype == Q4_K; }
+
+// Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
+// rows).
+int mmqs_max_tiles() { return 4; }
+
+hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hipStream_t st) {
+    const int tw = (rows_per_wg + 15) / 16;
+    const void* fn = nullptr;
+    if (dtype == Q4_K) {
+        fn = wg == 256   ? sfn_tw<Q4_K, 256>(tw, a.bias_mode != 0)
+             : wg == 1024 ? sfn_tw<Q4_K, 1024>(tw, a.bias_mode != 0)
+                          : sfn_tw<Q4_K, 512>(tw, a.bias_mode != 0);
+    }
+    if (!fn) return hipErrorInvalidValue;
+    const int grid = (a.N + rows_per_wg - 1) / rows_per_wg;
+    MmqArgs args = a;
+    int rpw = rows_per_wg;
+    void* params[] = {&args, &rpw};
+    return hipLaunchKernel(fn, dim3(grid), dim3(wg), params, 0, st);
+}
+
+}  // namespace fq
