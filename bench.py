@@ -65,6 +65,8 @@ def parse():
                    help="only time these shapes (e.g. q4_0:152064x3584:1), GGUF and, for "
                         "M = 1, aligned layout; one JSON line each on stdout")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--warm-seconds", type=float, default=0.2,
+                   help="graph replays before each per-config timing (clock ramp)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--layout", choices=("packed", "gguf"), default="packed",
                    help="device weight layout of the headline value: aligned repack "
@@ -192,6 +194,9 @@ def cpu_config(dtype, w_np, N, K, M, budget_s=1.0):
     return {"cpu_ref_us": round(us, 1), "cpu_rows": rows, "cpu_threads": threads}
 
 
+WARM_SECONDS = 0.2
+
+
 def time_config(name, dtype, N, K, M, reps=20, pool_bytes=600 << 20, packed=False, cpu=False,
                 w_np=None):
     """Average per-call device time of one matmul shape.  `reps` calls over
@@ -236,7 +241,7 @@ def time_config(name, dtype, N, K, M, reps=20, pool_bytes=600 << 20, packed=Fals
             call(ws[r % copies], side.cuda_stream)
     # replays for ~0.2 s first: the GPU idles while the host makes the
     # weights, and its clocks need that long to come back up
-    t_end = time.perf_counter() + 0.2
+    t_end = time.perf_counter() + WARM_SECONDS
     while time.perf_counter() < t_end:
         g.replay()
         torch.cuda.synchronize()
@@ -373,7 +378,9 @@ class StepRunner:
 
 
 def main():
+    global WARM_SECONDS
     args = parse()
+    WARM_SECONDS = args.warm_seconds
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this hot path is single-GPU by design "
               "(sharding the rows across GPUs is a design, not implemented); "
@@ -539,7 +546,7 @@ def time_fused(name, dtype, N, K, reps=20, pool_bytes=600 << 20):
         with torch.cuda.graph(g, stream=side):
             for r in range(reps):
                 fn(pairs[r % copies], side.cuda_stream)
-        t_end = time.perf_counter() + 0.2  # clocks back up after the host-side setup
+        t_end = time.perf_counter() + WARM_SECONDS  # clocks back up after the host-side setup
         while time.perf_counter() < t_end:
             g.replay()
             torch.cuda.synchronize()
