@@ -22,7 +22,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 SOURCES = ["fq_dequant.hip", "fq_gemv1.hip", "fq_gemvp.hip", "fq_pack.hip", "fq_mmq.hip",
-           "fq_mmqi.hip", "fq_mmqs.hip",
+           "fq_mmqi.hip", "fq_mmqs.hip", "fq_mmqp.hip",
            "fq_capi.cpp"]
 
 COMMON = [
@@ -32,10 +32,17 @@ COMMON = [
 ]
 
 
+# Per-file flags.  The prefill kernel adds one FMA per block to each of its 64
+# MFMA results per lane: with the results in AGPRs (the compiler's default
+# under that register pressure) every FMA needs a v_accvgpr_read first, so
+# the MFMA results are kept in VGPRs.
+EXTRA = {"fq_mmqp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
     lang = [] if src.endswith(".hip") else ["-x", "hip"]
-    cmd = [HIPCC, *COMMON, *lang, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, []), *lang, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

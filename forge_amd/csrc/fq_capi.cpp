@@ -449,6 +449,47 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         }
     }
 
+    if (fq::mmqp_supported((int)dtype) && M > 32 && K > 0 && K % 64 == 0) {
+        // prefill, Q8_0 / Q4_0: per-token operands, then 128 x 128 tiles on
+        // v_mfma_f32_32x32x16_f16 (K-split while the tiles leave CUs idle)
+        const int Tn = (M + 31) / 32, nsteps = K / 64;
+        const long tiles = (long)((N + 127) / 128) * ((M + 127) / 128);
+        int splits = tiles >= di.cus ? 1 : (int)std::min<long>(8, (2L * di.cus + tiles - 1) / tiles);
+        splits = std::max(1, std::min(splits, nsteps / 4));
+        auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+        const size_t xop_b = (size_t)Tn * K * 64 * 2, ex_b = (size_t)M * 4,
+                     part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+        const size_t need = 256 + al(xop_b) + al(ex_b) + al(part_b);
+        std::unique_ptr<StreamScratch::Lease> lease;
+        uint8_t* buf = fixed;
+        if (fixed) {
+            if (need > fixed_cap) return FQ_ERR_WORKSPACE;
+        } else {
+            lease.reset(new StreamScratch::Lease(stream_scratch(dev, st, 0)));
+            const int rc = lease->get(need, st, &buf);
+            if (rc != FQ_OK) return rc;
+        }
+        fq::MmqArgs a{};
+        a.w = static_cast<const uint8_t*>(w);
+        a.xop = buf;
+        a.ex = reinterpret_cast<const int*>(buf + al(xop_b));
+        a.part = splits > 1 ? reinterpret_cast<float*>(buf + al(xop_b) + al(ex_b)) : nullptr;
+        a.y = y;
+        a.bias = bias;
+        a.bias_len = bias_mode ? bias_len : 0;
+        a.bias_mode = bias_mode;
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.row_bytes = (K / g.be) * g.bb;
+        e = fq::launch_xprep32(x, M, K, reinterpret_cast<_Float16*>(buf),
+                               const_cast<int*>(a.ex), st);
+        if (e != hipSuccess) return hip_fail(e);
+        e = fq::launch_mmqp((int)dtype, a, splits, st);
+        if (e == hipSuccess && splits > 1) e = fq::launch_reduce(a, splits, st);
+        return e == hipSuccess ? FQ_OK : hip_fail(e);
+    }
+
     // M > 4, and rows too long for the batch-1 kernels' LDS
     return run_mmq(dtype, g, x, w, bias, bias_mode, bias_len, y, M, K, N, dev, di, st, fixed,
                    fixed_cap);

@@ -81,6 +81,13 @@ hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, in
 bool mmqs_supported(int dtype);
 int mmqs_max_tiles();
 hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hipStream_t st);
+// prefill for Q8_0 / Q4_0 on v_mfma_f32_32x32x16_f16 (fq_mmqp.hip): token
+// operands of launch_xprep32 (a.xop, a.ex = one exponent per token), a.part
+// holds the split-K slabs when splits > 1 (then reduce with launch_reduce)
+bool mmqp_supported(int dtype);
+hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, hipStream_t st);
+hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st);
+hipError_t launch_reduce(const MmqArgs& a, int splits, hipStream_t st);
 hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,
                           int row_bytes, int grid, hipStream_t st);
 

@@ -203,4 +203,34 @@ __device__ __forceinline__ void read_limbs(Limbs& L, const uint8_t* lds, int u) 
     L.S[3] = reinterpret_cast<const float*>(lds + RECB * u)[28];
 }
 
+// 16 / 8 bytes at a 2-byte-aligned LDS address.  A misaligned ds_read_b128
+// runs at a fraction of the aligned rate (about 9 cycles of LDS issue per
+// instruction against under 2 aligned), so the bytes are read as aligned
+// dwords and shifted into place with v_alignbyte_b32 (shift 0 or 2 bytes).
+__device__ __forceinline__ uint32_t lds_dword(const uint8_t* p) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(
+        reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ uint4 lds16_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint8_t* q = reinterpret_cast<const uint8_t*>(a & ~(uintptr_t)3);
+    const uint32_t s = (uint32_t)(a & 3);
+    const uint32_t w0 = lds_dword(q), w1 = lds_dword(q + 4), w2 = lds_dword(q + 8),
+                   w3 = lds_dword(q + 12), w4 = lds_dword(q + 16);
+    return {__builtin_amdgcn_alignbyte(w1, w0, s), __builtin_amdgcn_alignbyte(w2, w1, s),
+            __builtin_amdgcn_alignbyte(w3, w2, s), __builtin_amdgcn_alignbyte(w4, w3, s)};
+}
+__device__ __forceinline__ uint32_t lds4_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint8_t* q = reinterpret_cast<const uint8_t*>(a & ~(uintptr_t)3);
+    return __builtin_amdgcn_alignbyte(lds_dword(q + 4), lds_dword(q), (uint32_t)(a & 3));
+}
+__device__ __forceinline__ uint2 lds8_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint8_t* q = reinterpret_cast<const uint8_t*>(a & ~(uintptr_t)3);
+    const uint32_t s = (uint32_t)(a & 3);
+    const uint32_t w0 = lds_dword(q), w1 = lds_dword(q + 4), w2 = lds_dword(q + 8);
+    return {__builtin_amdgcn_alignbyte(w1, w0, s), __builtin_amdgcn_alignbyte(w2, w1, s)};
+}
+
 }  // namespace fq

@@ -651,6 +651,13 @@ hipError_t launch_xprep(int dtype, const float* x, int M, int K, int NC, _Float1
     return hipGetLastError();
 }
 
+hipError_t launch_reduce(const MmqArgs& a, int splits, hipStream_t st) {
+    const size_t total = (size_t)a.M * a.N;
+    const int grid = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+    hipLaunchKernelGGL(reduce_kernel, dim3(grid), dim3(256), 0, st, a, splits);
+    return hipGetLastError();
+}
+
 hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, int splits,
                       hipStream_t st) {
     const hipError_t e = with_format(dtype, hipErrorInvalidValue, [&](auto f) {
