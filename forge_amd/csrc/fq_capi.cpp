@@ -449,12 +449,16 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         }
     }
 
-    if (fq::mmqp_supported((int)dtype) && M > 32 && K > 0 && K % 64 == 0) {
-        // prefill, Q8_0 / Q4_0: per-token operands, then 128 x 128 tiles on
-        // v_mfma_f32_32x32x16_f16 (K-split while the tiles leave CUs idle)
+    if (fq::mmqp_supported((int)dtype) && M > 32 && K > 0 && K % 256 == 0 &&
+        (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+        // prefill, Q8_0 / Q4_0 rows that are whole 16-byte chunks (K a
+        // multiple of 256, 16-byte aligned weights): per-token operands, then
+        // one work-group per CU and tile on v_mfma_f32_32x32x16_f16 (K-split
+        // while the tiles leave CUs idle)
         const int Tn = (M + 31) / 32, nsteps = K / 64;
-        const long tiles = (long)((N + 127) / 128) * ((M + 127) / 128);
-        int splits = tiles >= di.cus ? 1 : (int)std::min<long>(8, (2L * di.cus + tiles - 1) / tiles);
+        const int tn = fq::mmqp_tile_rows(), tm = fq::mmqp_tile_tokens();
+        const long tiles = (long)((N + tn - 1) / tn) * ((M + tm - 1) / tm);
+        int splits = tiles >= di.cus ? 1 : (int)std::min<long>(16, (di.cus + tiles - 1) / tiles);
         splits = std::max(1, std::min(splits, nsteps / 4));
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
         const size_t xop_b = (size_t)Tn * K * 64 * 2, ex_b = (size_t)M * 4,

@@ -85,6 +85,8 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hip
 // operands of launch_xprep32 (a.xop, a.ex = one exponent per token), a.part
 // holds the split-K slabs when splits > 1 (then reduce with launch_reduce)
 bool mmqp_supported(int dtype);
+int mmqp_tile_rows();    // rows per work-group tile
+int mmqp_tile_tokens();  // tokens per work-group tile
 hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, hipStream_t st);
 hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st);
 hipError_t launch_reduce(const MmqArgs& a, int splits, hipStream_t st);

@@ -1,27 +1,13 @@
 // fq_mmqp.hip -- prefill (M > 32 tokens) for the 32-weight block formats
 // Q8_0 and Q4_0 on v_mfma_f32_32x32x16_f16.
 //
-//   D[token][n] = X[token][k] . W[n][k]^T, per 32-element block b:
-//     A (32 tokens x 16 k): x 2^-e(token) as fp16 hi + lo (xprep32_kernel),
-//     B (16 k x 32 rows):   the block's integer codes, exact in fp16,
-//     D_b = A_hi B + A_lo B  (two MFMAs per 16 k, one fp32 result per block),
-//     acc += d_b(n) D_b      (one FMA per output and block),
-//   y = 2^e(token) acc at the end.
-// Weights are the B operand so that a lane's 16 results all belong to one
-// row n: the block scale d_b(n) is one value per lane.  One exponent per
-// token over all of K (the token's largest |x| scaled into [2^14, 2^15))
-// keeps the per-block epilogue to that single FMA; x_hi + x_lo carry 22
-// significant bits.
+//   D[token][n] = X[token][k] . W[n][k]^T on the fp16 matrix cores, with the
+// tokens as x 2^-e(token) in fp16 hi + lo and the weights' integer codes
+// exact in fp16; one FMA per output and block folds in the block scale
+// (mmqp_kernel below).
 //
-// A work-group owns 128 tokens x 128 rows (4 waves, 64 x 64 each: 2 x 2
-// MFMA tiles) and a K range (split-K when the tiles alone leave CUs idle;
-// reduce_kernel adds the slabs in split order).  Per 64-element K-step every
-// global load of the next step is issued at once -- the token operands (four
-// contiguous 8 KiB runs, copied straight into the other of two LDS buffers)
-// and the 128 weight rows' 68 / 36 bytes (into registers, written to LDS
-// after the step's compute).  So each step waits once, at its barrier, for
-// loads issued a whole step earlier, and no short load queues behind a long
-// one in the in-order vector memory counter.
+// Token prep is two launches: the per-token exponent (one pass over x), then
+// the hi/lo operands in the A-operand layout (a second pass).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -35,22 +21,22 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BMT = 128, BNT = 128;  // tokens, rows per work-group
+constexpr int BMT = 128, BNT = 256;  // tokens, rows per work-group
 constexpr int KS = 64;               // K elements per step (two blocks)
 constexpr int XT = 1024;             // halves per (32-token tile, 16-k quarter): hi then lo
+constexpr int NBUF = 3;              // LDS buffers per operand: steps s, s + 1, s + 2
+constexpr int NW = 8;                // waves per work-group
 
 // ------------------------------------------------------------- token prep
-// One work-group per token: e = ilogb(max |x|) - 14, then x 2^-e split into
-// fp16 hi + lo, written as the A operand of v_mfma_f32_32x32x16_f16: for
-// token tile T = m / 32 and quarter kq = k / 16, lane (m % 32) + 32 g holds
-// elements 16 kq + 8 g + slot_elem(j), j = 0..7 (hi block, then lo block).
-__global__ __launch_bounds__(256) void xprep32_kernel(const float* __restrict__ x, int K,
-                                                      _Float16* __restrict__ xop,
-                                                      int* __restrict__ ex) {
+// One work-group per token: e = ilogb(max |x|) - 14 (0 for an all-zero
+// token), so that x 2^-e lies below 2^15 in magnitude.
+__global__ __launch_bounds__(256) void xexp_kernel(const float* __restrict__ x, int K,
+                                                   int* __restrict__ ex) {
     __shared__ float wmax[4];
     const int m = blockIdx.x;
     const float* xr = x + (size_t)m * K;
     float mx = 0.0f;
+#pragma unroll 4
     for (int k = threadIdx.x * 4; k < K; k += 1024) {
         const float4 v = *reinterpret_cast<const float4*>(xr + k);
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -59,30 +45,65 @@ __global__ __launch_bounds__(256) void xprep32_kernel(const float* __restrict__ 
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    int e = 0;
-    if (mx > 0.0f && mx <= 3.0e38f) e = ilogbf(mx) - 14;
-    if (threadIdx.x == 0) ex[m] = e;
-    const int T = m >> 5, lm = m & 31;
-    for (int grp = threadIdx.x; grp < K / 8; grp += 256) {
-        const float4 a = *reinterpret_cast<const float4*>(xr + 8 * grp);
-        const float4 b = *reinterpret_cast<const float4*>(xr + 8 * grp + 4);
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        h8 hi, lo;
+    if (threadIdx.x == 0) {
+        mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        ex[m] = (mx > 0.0f && mx <= 3.0e38f) ? ilogbf(mx) - 14 : 0;
+    }
+}
+
+// x 2^-e(token) split into fp16 hi + lo, written as the A operand of
+// v_mfma_f32_32x32x16_f16: for token tile T = m / 32 and quarter kq = k / 16,
+// lane (m % 32) + 32 g holds elements 16 kq + 8 g + slot_elem(j), j = 0..7,
+// the hi block then the lo block 512 halves on.  Work-group (step group,
+// T): wave w writes quarters 4 w .. 4 w + 3 of the group's 16, 2 KiB each,
+// contiguously.  Token slots past M are zero.
+constexpr int XG = 16;  // quarters (16 k each) per work-group
+__global__ __launch_bounds__(256) void xprep32_kernel(const float* __restrict__ x, int M, int K,
+                                                      const int* __restrict__ ex,
+                                                      _Float16* __restrict__ xop) {
+    const int T = blockIdx.y, lane = threadIdx.x & 63;
+    const int lm = lane & 31, g = lane >> 5, m = 32 * T + lm;
+    const int kq0 = XG * blockIdx.x + 4 * (threadIdx.x >> 6);
+    const int e = m < M ? ex[m] : 0;
+    const float* src = x + (size_t)min(m, M - 1) * K + 16 * kq0 + 8 * g;
+    float4 v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float w = __builtin_amdgcn_ldexpf(v[slot_elem(j)], -e);
-            hi[j] = (_Float16)w;
-            lo[j] = (_Float16)(w - (float)hi[j]);
+    for (int q = 0; q < 4; ++q) {
+        v[2 * q] = *reinterpret_cast<const float4*>(src + 16 * q);
+        v[2 * q + 1] = *reinterpret_cast<const float4*>(src + 16 * q + 4);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float f[8] = {v[2 * q].x,     v[2 * q].y,     v[2 * q].z,     v[2 * q].w,
+                            v[2 * q + 1].x, v[2 * q + 1].y, v[2 * q + 1].z, v[2 * q + 1].w};
+        h8 hi = {}, lo = {};
+        if (m < M) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float w = __builtin_amdgcn_ldexpf(f[slot_elem(j)], -e);
+                hi[j] = (_Float16)w;
+                lo[j] = (_Float16)(w - (float)hi[j]);
+            }
         }
-        const int kq = grp >> 1, g = grp & 1;
-        _Float16* dst = xop + ((size_t)T * (K / 16) + kq) * XT + (lm + 32 * g) * 8;
+        _Float16* dst = xop + ((size_t)T * (K / 16) + kq0 + q) * XT + lane * 8;
         *reinterpret_cast<h8*>(dst) = hi;
         *reinterpret_cast<h8*>(dst + 512) = lo;
     }
 }
 
 // -------------------------------------------------------- weight operands
+// Eight bytes as fp16 (value - off): v_perm pairs each byte with 0x64, so a
+// half reads 1024 + byte, in the slot order {0, 2, 1, 3} of each dword.
+__device__ __forceinline__ h8 perm8(uint32_t w0, uint32_t w1, _Float16 off) {
+    const h2 o = {off, off};
+    const uint32_t c = 0x64646464u;
+    const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c, w0, 0x04020400u)) - o;
+    const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c, w0, 0x04030401u)) - o;
+    const h2 d = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c, w1, 0x04020400u)) - o;
+    const h2 e = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c, w1, 0x04030401u)) - o;
+    return h8{a[0], a[1], b[0], b[1], d[0], d[1], e[0], e[1]};
+}
+
 template <int F>
 struct PB;
 
@@ -94,7 +115,7 @@ struct PB<Q8_0> {
     static constexpr int BB = 34, SB = 2 * BB;  // bytes per block, per step
     __device__ static h8 op(const uint8_t* blk, int h, int g) {
         const uint2 q = lds8_a2(blk + 2 + 16 * h + 8 * g);
-        return byte8(q.x ^ 0x80808080u, q.y ^ 0x80808080u, (_Float16)1152.0f);
+        return perm8(q.x ^ 0x80808080u, q.y ^ 0x80808080u, (_Float16)1152.0f);
     }
 };
 
@@ -109,56 +130,112 @@ struct PB<Q4_0> {
     }
 };
 
+// Global memory straight into LDS: 16 or 4 bytes per lane, to lds + 16 lane
+// or lds + 4 lane (lds is wave-uniform, in M0).  Issued as inline assembly on
+// purpose: the compiler cannot tell which LDS bytes the builtin's copy
+// writes, so it waits for every outstanding load (vmcnt(0)) before the next
+// LDS read, which would serialise each step's loads with the step's compute.
+// The kernel counts the copies itself (wait_steps) before the barrier that
+// publishes them.
+__device__ __forceinline__ void dma16(const uint8_t* g, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const uint8_t* g, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(g), "{m0}"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 template <int F>
-__global__ __launch_bounds__(256) void mmqp_kernel(MmqArgs a, int steps_per_split) {
+struct Tile {
     using P = PB<F>;
-    constexpr int WROW = (P::SB + 3) / 4 * 4;     // LDS bytes per weight row and step
-    constexpr int WDW = BNT * WROW / 4;            // dwords of the weight tile
-    constexpr int WPT = (WDW + 255) / 256;         // weight dwords per thread
-    // token operands: two buffers (the next step's arrive by DMA while this
-    // step reads the other), 4 token tiles x 4 quarters each
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][4 * 4 * XT];
-    __shared__ __attribute__((aligned(16))) uint8_t ws[BNT * WROW];
+    // A step of a row (68 / 36 bytes) starts (s SB) mod 16 = 0, 4, 8 or 12
+    // bytes into a 16-byte chunk (rows are 16-byte aligned), so CH chunks
+    // cover it for every step.
+    static constexpr int CH = (P::SB + 12 + 15) / 16;   // chunks per row and step
+    static constexpr int WROW = 16 * CH;                // LDS bytes per weight row and step
+    static constexpr int WCH = BNT * CH;                // chunks of a step's weight tile
+    static constexpr int WIN = WCH / 64;                // copy instructions per step (whole)
+    static_assert(WCH % 64 == 0, "whole copy instructions");
+    static constexpr int WI_LO = WIN / NW, WI_HI = (WIN + NW - 1) / NW;
+    static constexpr int W_HI = WIN - NW * WI_LO;       // waves that issue WI_HI copies
+    static constexpr int WBUF = BNT * WROW;             // bytes per weight buffer
+    static constexpr int XI = 4;                        // token copies per wave (1 KiB each)
+    static constexpr int XBUF = 16 * XT * 2;            // bytes per token buffer
+    static constexpr int LDS = NBUF * (XBUF + WBUF);
+};
+
+// A work-group owns 128 tokens x 256 rows and a K range (split-K when the
+// tiles alone leave CUs idle; reduce_kernel adds the slabs in split order).
+// Eight waves, each 64 tokens x 64 rows (2 x 2 tiles of 32 x 32).
+//
+// Per 32-element block b:
+//   A (32 tokens x 16 k): x 2^-e(token) as fp16 hi + lo (xprep32_kernel),
+//   B (16 k x 32 rows):   the block's integer codes, exact in fp16,
+//   D_b = A_hi B + A_lo B  (two MFMAs per 16 k, one fp32 result per block),
+//   acc += d_b(n) D_b      (one FMA per output and block),
+// y = 2^e(token) acc at the end.  Weights are the B operand so that a lane's
+// 16 results all belong to one row n: the block scale d_b(n) is one value
+// per lane.  x_hi + x_lo carry 22 significant bits.
+//
+// Both operands reach LDS by direct copies into three buffers: while step s
+// is computed, the copies of steps s + 1 and s + 2 are in flight, and one
+// barrier per step publishes the next step's buffers.
+template <int F>
+__global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_split) {
+    using P = PB<F>;
+    using TL = Tile<F>;
+    constexpr int WROW = TL::WROW;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[TL::LDS];
+    uint8_t* const xs0 = lds;                       // NBUF token buffers
+    uint8_t* const ws0 = lds + NBUF * TL::XBUF;     // NBUF weight buffers
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = tid >> 6, wm = wave >> 1, wn = wave & 1;  // 64-token / 64-row quadrant
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;  // 64-token / 64-row quadrant
     const int n0 = blockIdx.x * BNT, m0 = blockIdx.y * BMT;
     const int nsteps = a.K / KS;
     const int s0 = blockIdx.z * steps_per_split, s1 = min(nsteps, s0 + steps_per_split);
-    const int T0 = m0 / 32;                 // first token tile
     const int Tn = (a.M + 31) / 32;         // token tiles in the operand buffer
     const int KQ = a.K / 16;
 
-    // loads of step s: the token operands straight into LDS buffer s & 1
-    // (wave w copies token tile w's contiguous 8 KiB run, 1 KiB per
-    // instruction), the weight rows into registers
-    uint32_t wr[WPT];
-    auto gload = [&](int s) {
-        {
-            const int T = min(T0 + wave, Tn - 1);
-            const uint8_t* src = reinterpret_cast<const uint8_t*>(
-                reinterpret_cast<const _Float16*>(a.xop) + ((size_t)T * KQ + 4 * s) * XT);
-            uint8_t* dst = reinterpret_cast<uint8_t*>(xs[s & 1]) + wave * 8192;
+    // copy sources of this lane: token run (tile T0 + wave / 2, half wave & 1
+    // of its 8 KiB per step), and the 16-byte weight chunks L = 64 (NW q +
+    // wave) + lane of the row-major [row][CH] step tile (rows clamped to a
+    // real row)
+    const int T = min(m0 / 32 + (wave >> 1), Tn - 1);
+    const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(a.xop) +
+                          ((size_t)T * KQ * XT) * 2 + (wave & 1) * 4096 + 16 * lane;
+    const int nwi = wave < TL::W_HI ? TL::WI_HI : TL::WI_LO;  // wave-uniform
+    const uint8_t* wsrc[TL::WI_HI];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void*)(src + 1024 * i + 16 * lane),
-                    (__attribute__((address_space(3))) void*)(dst + 1024 * i), 16, 0, 0);
-        }
+    for (int q = 0; q < TL::WI_HI; ++q) {
+        const int L = min(64 * (NW * q + wave) + lane, TL::WCH - 1);
+        const int r = L / TL::CH, p = L - r * TL::CH;
+        wsrc[q] = a.w + (size_t)min(n0 + r, a.N - 1) * a.row_bytes + 16 * p;
+    }
+    const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds);
+    auto issue = [&](int s) {
+        const int buf = s % NBUF;
+        const uint32_t xl = lds_base + buf * TL::XBUF + wave * 4096;
+        const uint8_t* xg = xsrc + (size_t)s * 4 * XT * 2;
 #pragma unroll
-        for (int i = 0; i < WPT; ++i) {
-            const int idx = min(tid + 256 * i, WDW - 1);
-            const int r = idx / (WROW / 4), c = idx - r * (WROW / 4);
-            const int row = min(n0 + r, a.N - 1);
-            const uint8_t* src = a.w + (size_t)row * a.row_bytes + (size_t)s * P::SB + 4 * c;
-            wr[i] = ld_u32(src);  // a step of a row is 68 / 36 bytes: whole dwords
-        }
+        for (int i = 0; i < TL::XI; ++i) dma16(xg + 1024 * i, xl + 1024 * i);
+        const uint32_t wl = lds_base + NBUF * TL::XBUF + buf * TL::WBUF + wave * 1024;
+        const size_t koff = (size_t)s * P::SB & ~(size_t)15;
+#pragma unroll
+        for (int q = 0; q < TL::WI_HI; ++q)
+            if (q < nwi) dma16(wsrc[q] + koff, wl + NW * 1024 * q);
     };
-    auto lstore = [&]() {
-#pragma unroll
-        for (int i = 0; i < WPT; ++i) {
-            const int idx = tid + 256 * i;
-            if (idx < WDW) reinterpret_cast<uint32_t*>(ws)[idx] = wr[i];
-        }
+    // this wave's copies of step s are complete (those of step s + 1 may
+    // still be in flight)
+    auto wait_step = [&](bool next_in_flight) {
+        if (!next_in_flight) wait_vm<0>();
+        else if (nwi == TL::WI_HI) wait_vm<TL::XI + TL::WI_HI>();
+        else wait_vm<TL::XI + TL::WI_LO>();
     };
 
     f32x16 acc[2][2];
@@ -170,12 +247,18 @@ __global__ __launch_bounds__(256) void mmqp_kernel(MmqArgs a, int steps_per_spli
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     const int g = lane >> 5, c = lane & 31;
-    if (s0 < s1) gload(s0);
+    if (s0 < s1) issue(s0);
+    if (s0 + 1 < s1) issue(s0 + 1);
     for (int s = s0; s < s1; ++s) {
-        __syncthreads();  // the previous step's LDS reads are done
-        lstore();
+        // this wave's copies of step s are done; the barrier makes every
+        // wave's visible and ends every wave's reads of step s - 1, whose
+        // buffers step s + 2 then refills
+        wait_step(s + 1 < s1);
         __syncthreads();
-        if (s + 1 < s1) gload(s + 1);
+        if (s + 2 < s1) issue(s + 2);
+        const int buf = s % NBUF;
+        const _Float16* xs = reinterpret_cast<const _Float16*>(xs0 + buf * TL::XBUF);
+        const uint8_t* ws = ws0 + buf * TL::WBUF + ((s * P::SB) & 15);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             // token operands of both 16-k halves of the block, then per
@@ -185,8 +268,7 @@ __global__ __launch_bounds__(256) void mmqp_kernel(MmqArgs a, int steps_per_spli
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    const _Float16* xp =
-                        xs[s & 1] + ((2 * wm + i) * 4 + 2 * b + h) * XT + lane * 8;
+                    const _Float16* xp = xs + ((2 * wm + i) * 4 + 2 * b + h) * XT + lane * 8;
                     ah[h][i] = *reinterpret_cast<const h8*>(xp);
                     al[h][i] = *reinterpret_cast<const h8*>(xp + 512);
                 }
@@ -247,9 +329,16 @@ __global__ __launch_bounds__(256) void mmqp_kernel(MmqArgs a, int steps_per_spli
 }  // namespace
 
 bool mmqp_supported(int dtype) { return dtype == Q8_0 || dtype == Q4_0; }
+int mmqp_tile_rows() { return BNT; }
+int mmqp_tile_tokens() { return BMT; }
 
 hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, hipStream_t st) {
-    hipLaunchKernelGGL(xprep32_kernel, dim3(M), dim3(256), 0, st, x, K, xop, ex);
+    if (K % (16 * XG) != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(xexp_kernel, dim3(M), dim3(256), 0, st, x, K, ex);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(xprep32_kernel, dim3(K / (16 * XG), (M + 31) / 32), dim3(256), 0, st, x,
+                       M, K, ex, xop);
     return hipGetLastError();
 }
 
@@ -258,9 +347,9 @@ hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st) 
     const int sps = (nsteps + splits - 1) / splits;
     const dim3 grid((a.N + BNT - 1) / BNT, (a.M + BMT - 1) / BMT, splits);
     if (dtype == Q8_0)
-        hipLaunchKernelGGL(mmqp_kernel<Q8_0>, grid, dim3(256), 0, st, a, sps);
+        hipLaunchKernelGGL(mmqp_kernel<Q8_0>, grid, dim3(64 * NW), 0, st, a, sps);
     else if (dtype == Q4_0)
-        hipLaunchKernelGGL(mmqp_kernel<Q4_0>, grid, dim3(256), 0, st, a, sps);
+        hipLaunchKernelGGL(mmqp_kernel<Q4_0>, grid, dim3(64 * NW), 0, st, a, sps);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
