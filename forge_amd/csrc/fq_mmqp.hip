@@ -247,6 +247,21 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     const int g = lane >> 5, c = lane & 31;
+    // The operands of the next (block, token tile) are read from LDS while
+    // the current one's MFMAs run, and a stage's block-scale fold (FMAs on
+    // its chain results) waits until the next stage's MFMAs are issued, so
+    // the matrix cores and the LDS reads of a wave overlap.
+    auto read_a = [&](const _Float16* xs, int b, int i, h8 (&r)[4]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const _Float16* xp = xs + ((2 * wm + i) * 4 + 2 * b + h) * XT + lane * 8;
+            r[2 * h] = *reinterpret_cast<const h8*>(xp);
+            r[2 * h + 1] = *reinterpret_cast<const h8*>(xp + 512);
+        }
+    };
+    f32x16 dp[2];   // chain results of the previous stage (token tile 1 at a step's end)
+    float dbp[2];
+    bool pend = false;
     if (s0 < s1) issue(s0);
     if (s0 + 1 < s1) issue(s0 + 1);
     for (int s = s0; s < s1; ++s) {
@@ -259,44 +274,60 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
         const int buf = s % NBUF;
         const _Float16* xs = reinterpret_cast<const _Float16*>(xs0 + buf * TL::XBUF);
         const uint8_t* ws = ws0 + buf * TL::WBUF + ((s * P::SB) & 15);
+        h8 A[2][4];
+        read_a(xs, 0, 0, A[0]);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            // token operands of both 16-k halves of the block, then per
-            // weight tile the four MFMAs of both token tiles and the fold
-            h8 ah[2][2], al[2][2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const _Float16* xp = xs + ((2 * wm + i) * 4 + 2 * b + h) * XT + lane * 8;
-                    ah[h][i] = *reinterpret_cast<const h8*>(xp);
-                    al[h][i] = *reinterpret_cast<const h8*>(xp + 512);
-                }
+            // the block's weight operands (both row tiles, both halves) and scales
+            h8 B[2][2];
+            float db[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const uint8_t* wrow = ws + (64 * wn + 32 * j + c) * WROW + P::BB * b;
-                const h8 b0 = P::op(wrow, 0, g), b1 = P::op(wrow, 1, g);
-                const f32x16 z = {};
+                B[j][0] = P::op(wrow, 0, g);
+                B[j][1] = P::op(wrow, 1, g);
+                db[j] = f16_hw(*reinterpret_cast<const uint16_t*>(wrow));
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int st = 2 * b + i;  // stage within the step
+                h8(&cur)[4] = A[st & 1];
+                if (st < 3) read_a(xs, (st + 1) >> 1, (st + 1) & 1, A[(st + 1) & 1]);
                 f32x16 d[2];
+                const f32x16 z = {};
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    d[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0][i], b0, z, 0, 0, 0);
+                for (int j = 0; j < 2; ++j)
+                    d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[0], B[j][0], z, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    d[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0][i], b0, d[i], 0, 0, 0);
+                for (int j = 0; j < 2; ++j)
+                    d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[1], B[j][0], d[j], 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    d[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1][i], b1, d[i], 0, 0, 0);
+                for (int j = 0; j < 2; ++j)
+                    d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[2], B[j][1], d[j], 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    d[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1][i], b1, d[i], 0, 0, 0);
-                const float db = f16_hw(*reinterpret_cast<const uint16_t*>(wrow));
+                for (int j = 0; j < 2; ++j)
+                    d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[3], B[j][1], d[j], 0, 0, 0);
+                // fold the previous stage (token tile 1 - i)
+                if (pend) {
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                    for (int j = 0; j < 2; ++j)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(db, d[i][e], acc[i][j][e]);
+                        for (int e = 0; e < 16; ++e)
+                            acc[1 - i][j][e] = __builtin_fmaf(dbp[j], dp[j][e], acc[1 - i][j][e]);
+                }
+                dp[0] = d[0];
+                dp[1] = d[1];
+                dbp[0] = db[0];
+                dbp[1] = db[1];
+                pend = true;
             }
         }
+    }
+    if (pend) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[1][j][e] = __builtin_fmaf(dbp[j], dp[j][e], acc[1][j][e]);
     }
     // lane (c, g): column n = 32 j + c of its quadrant, rows 8 (e / 4) + 4 g + e % 4
     const bool split = gridDim.z > 1;
