@@ -75,8 +75,31 @@ def traffic(fetch_csv, write_csv, copy_mib, kernel, grid, lds):
             "hbm_bytes_per_launch": int(fetch_b + write_b)}
 
 
+def counters(path: str, match: str = ""):
+    """Average each counter per dispatch, grouped by (kernel, grid, LDS bytes)
+    -- the rocprofv3 --pmc counter_collection.csv, one row per (dispatch,
+    counter), values already summed over the chip's instances."""
+    agg = collections.OrderedDict()
+    for r in csv.DictReader(open(path)):
+        if match and match not in r["Kernel_Name"]:
+            continue
+        key = (r["Kernel_Name"], int(r["Grid_Size"]), int(r["LDS_Block_Size"]))
+        d = agg.setdefault(key, {})
+        tot, n = d.get(r["Counter_Name"], (0.0, 0))
+        d[r["Counter_Name"]] = (tot + float(r["Counter_Value"]), n + 1)
+    rows = []
+    for (name, grid, lds), d in agg.items():
+        rows.append({"kernel": name, "grid": grid, "lds": lds,
+                     "dispatches": max(n for _, n in d.values()),
+                     **{c: tot / n for c, (tot, n) in sorted(d.items())}})
+    return rows
+
+
 def main():
     p = argparse.ArgumentParser()
+    p.add_argument("--counters", metavar="COUNTER_CSV",
+                   help="average --pmc counters per dispatch and kernel shape")
+    p.add_argument("--match", default="", help="with --counters: kernel name substring")
     p.add_argument("trace", nargs="?")
     p.add_argument("--title", default="")
     p.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
@@ -85,6 +108,12 @@ def main():
     p.add_argument("--grid", type=int, default=0)
     p.add_argument("--lds", type=int, default=0)
     a = p.parse_args()
+    if a.counters:
+        for r in counters(a.counters, a.match):
+            print(f"- `{short(r.pop('kernel'))}` grid {r.pop('grid')} LDS {r.pop('lds')} "
+                  f"({r.pop('dispatches')} dispatches): " +
+                  ", ".join(f"{k} {v:.0f}" for k, v in r.items()))
+        return
     if a.traffic:
         import json
         print(json.dumps(traffic(a.traffic[0], a.traffic[1], a.copy_mib, a.kernel, a.grid,
