@@ -460,6 +460,10 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         const long tiles = (long)((N + tn - 1) / tn) * ((M + tm - 1) / tm);
         int splits = tiles >= di.cus ? 1 : (int)std::min<long>(16, (di.cus + tiles - 1) / tiles);
         splits = std::max(1, std::min(splits, nsteps / 4));
+        {   // the kernel walks its K range four steps at a time
+            const int sps = ((nsteps + splits - 1) / splits + 3) & ~3;
+            splits = (nsteps + sps - 1) / sps;
+        }
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
         const size_t xop_b = (size_t)Tn * K * 64 * 2, ex_b = (size_t)M * 4,
                      part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;

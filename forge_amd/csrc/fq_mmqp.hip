@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fq_formats.h"
 #include "fq_kernels.h"
 #include "fq_limbs.h"
@@ -52,9 +54,10 @@ __global__ __launch_bounds__(256) void xexp_kernel(const float* __restrict__ x, 
 }
 
 // x 2^-e(token) split into fp16 hi + lo, written as the A operand of
-// v_mfma_f32_32x32x16_f16: for token tile T = m / 32 and quarter kq = k / 16,
-// lane (m % 32) + 32 g holds elements 16 kq + 8 g + slot_elem(j), j = 0..7,
-// the hi block then the lo block 512 halves on.  Work-group (step group,
+// v_mfma_f32_32x32x16_f16: for token tile T = m / 32 and quarter kq (the
+// MFMA half kq % 2 of block kq / 2), lane (m % 32) + 32 g holds elements
+// 32 (kq / 2) + 16 g + 8 (kq % 2) + slot_elem(j), j = 0..7, the hi block
+// then the lo block 512 halves on.  Work-group (step group,
 // T): wave w writes quarters 4 w .. 4 w + 3 of the group's 16, 2 KiB each,
 // contiguously.  Token slots past M are zero.
 constexpr int XG = 16;  // quarters (16 k each) per work-group
@@ -65,12 +68,13 @@ __global__ __launch_bounds__(256) void xprep32_kernel(const float* __restrict__ 
     const int lm = lane & 31, g = lane >> 5, m = 32 * T + lm;
     const int kq0 = XG * blockIdx.x + 4 * (threadIdx.x >> 6);
     const int e = m < M ? ex[m] : 0;
-    const float* src = x + (size_t)min(m, M - 1) * K + 16 * kq0 + 8 * g;
+    const float* src = x + (size_t)min(m, M - 1) * K + 16 * kq0 + 16 * g;
     float4 v[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        v[2 * q] = *reinterpret_cast<const float4*>(src + 16 * q);
-        v[2 * q + 1] = *reinterpret_cast<const float4*>(src + 16 * q + 4);
+    for (int q = 0; q < 4; ++q) {  // kq0 is a multiple of 4: quarter kq0 + q
+        const float* sq = src + 32 * (q >> 1) + 8 * (q & 1);
+        v[2 * q] = *reinterpret_cast<const float4*>(sq);
+        v[2 * q + 1] = *reinterpret_cast<const float4*>(sq + 4);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -107,28 +111,60 @@ __device__ __forceinline__ h8 perm8(uint32_t w0, uint32_t w1, _Float16 off) {
 template <int F>
 struct PB;
 
-// Q8_0 block (34 B): d @0, qs int8[32] @2.  The B operand of half h (16 k)
-// for lane k-group g: qs bytes [16 h + 8 g, +8) as fp16 (+128 via the sign
-// bit, so the bytes are unsigned, then -1152 = -(1024 + 128)).
+// The K order inside a 32-element block: MFMA half h takes from lane group g
+// the elements 16 g + 8 h + j, so a lane's 16 elements of a block are
+// contiguous (one 16-byte read of Q8_0 codes; the 16 Q4_0 bytes, low nibbles
+// for g = 0, high for g = 1).  xprep32_kernel lays the tokens out the same
+// way.
+//
+// Q8_0 block (34 B): d @0, qs int8[32] @2.  Lane group g: bytes
+// qs[16 g, 16 g + 16) as fp16 (+128 via the sign bit, so the bytes are
+// unsigned, then -1152 = -(1024 + 128)); half h = bytes 8 h .. 8 h + 7.
 template <>
 struct PB<Q8_0> {
     static constexpr int BB = 34, SB = 2 * BB;  // bytes per block, per step
-    __device__ static h8 op(const uint8_t* blk, int h, int g) {
-        const uint2 q = lds8_a2(blk + 2 + 16 * h + 8 * g);
-        return perm8(q.x ^ 0x80808080u, q.y ^ 0x80808080u, (_Float16)1152.0f);
+    static constexpr int GS = 16;               // byte offset of lane group g
+    __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
+        b0 = perm8(q[0] ^ 0x80808080u, q[1] ^ 0x80808080u, (_Float16)1152.0f);
+        b1 = perm8(q[2] ^ 0x80808080u, q[3] ^ 0x80808080u, (_Float16)1152.0f);
     }
 };
 
 // Q4_0 block (18 B): d @0, qs[16] @2; element j < 16 is the low nibble of
-// byte j, element j + 16 the high nibble (value - 8).
+// byte j, element j + 16 the high nibble (value - 8).  Lane group g: nibble
+// g of bytes 8 h .. 8 h + 7 for half h.
 template <>
 struct PB<Q4_0> {
     static constexpr int BB = 18, SB = 2 * BB;
-    __device__ static h8 op(const uint8_t* blk, int h, int g) {
-        const uint2 q = lds8_a2(blk + 2 + 8 * g);
-        return nib8(q.x, q.y, 4 * h, (_Float16)1032.0f);
+    static constexpr int GS = 0;
+    __device__ static void ops(const uint32_t (&q)[4], int g, h8& b0, h8& b1) {
+        b0 = nib8(q[0], q[1], 4 * g, (_Float16)1032.0f);
+        b1 = nib8(q[2], q[3], 4 * g, (_Float16)1032.0f);
     }
 };
+
+// The 16 code bytes of lane group g of block b, for a row whose step starts
+// O4 bytes into its LDS slot (the slot holds the step's 16-byte chunks, so
+// O4 = (s SB) mod 16, a multiple of 4).  One or two aligned 16-byte reads
+// (16-byte reads at the slots' 80 / 48-byte stride fall on distinct banks),
+// then dword selection and byte alignment by constants.
+template <int F, int O4, int B>
+__device__ __forceinline__ void codes16(const uint8_t* row, int g, uint32_t (&q)[4]) {
+    using P = PB<F>;
+    constexpr int X = O4 + P::BB * B + 2;  // first code byte, lane group 0
+    constexpr int SH = X & 15, SD = SH >> 2, R = SH & 3;
+    const uint8_t* c0 = row + (X & ~15) + P::GS * g;
+    typedef const __attribute__((address_space(3))) fq_u32x4* lds_v4;
+    const fq_u32x4 v0 = *reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(c0));
+    fq_u32x4 v1 = v0;
+    if constexpr (SH != 0) v1 = *reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(c0 + 16));
+    const uint32_t w[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if constexpr (R == 0) q[k] = w[SD + k];
+        else q[k] = __builtin_amdgcn_alignbyte(w[SD + k + 1], w[SD + k], R);
+    }
+}
 
 // Global memory straight into LDS: 16 or 4 bytes per lane, to lds + 16 lane
 // or lds + 4 lane (lds is wave-uniform, in M0).  Issued as inline assembly on
@@ -262,18 +298,8 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
     f32x16 dp[2];   // chain results of the previous stage (token tile 1 at a step's end)
     float dbp[2];
     bool pend = false;
-    if (s0 < s1) issue(s0);
-    if (s0 + 1 < s1) issue(s0 + 1);
-    for (int s = s0; s < s1; ++s) {
-        // this wave's copies of step s are done; the barrier makes every
-        // wave's visible and ends every wave's reads of step s - 1, whose
-        // buffers step s + 2 then refills
-        wait_step(s + 1 < s1);
-        __syncthreads();
-        if (s + 2 < s1) issue(s + 2);
-        const int buf = s % NBUF;
-        const _Float16* xs = reinterpret_cast<const _Float16*>(xs0 + buf * TL::XBUF);
-        const uint8_t* ws = ws0 + buf * TL::WBUF + ((s * P::SB) & 15);
+    auto step = [&](auto o4, const _Float16* xs, const uint8_t* ws) {
+        constexpr int O4 = decltype(o4)::value;
         h8 A[2][4];
         read_a(xs, 0, 0, A[0]);
 #pragma unroll
@@ -283,10 +309,12 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
             float db[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const uint8_t* wrow = ws + (64 * wn + 32 * j + c) * WROW + P::BB * b;
-                B[j][0] = P::op(wrow, 0, g);
-                B[j][1] = P::op(wrow, 1, g);
-                db[j] = f16_hw(*reinterpret_cast<const uint16_t*>(wrow));
+                const uint8_t* row = ws + (64 * wn + 32 * j + c) * WROW;
+                uint32_t q[4];
+                if (b == 0) codes16<F, O4, 0>(row, g, q);
+                else codes16<F, O4, 1>(row, g, q);
+                P::ops(q, g, B[j][0], B[j][1]);
+                db[j] = f16_hw(*reinterpret_cast<const uint16_t*>(row + O4 + P::BB * b));
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -322,6 +350,27 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
                 pend = true;
             }
         }
+    };
+    if (s0 < s1) issue(s0);
+    if (s0 + 1 < s1) issue(s0 + 1);
+    // one step: this wave's copies of step s are done; the barrier makes
+    // every wave's visible and ends every wave's reads of step s - 1, whose
+    // buffers step s + 2 then refills
+    auto run = [&](auto o4, int s) {
+        wait_step(s + 1 < s1);
+        __syncthreads();
+        if (s + 2 < s1) issue(s + 2);
+        const int buf = s % NBUF;
+        step(o4, reinterpret_cast<const _Float16*>(xs0 + buf * TL::XBUF), ws0 + buf * TL::WBUF);
+    };
+    // a row's step s starts 4 (s mod 4) bytes into its LDS slot (68 and 36
+    // are 4 mod 16; s0 is a multiple of 4), so four steps per iteration
+    // give every read a constant offset
+    for (int s = s0; s < s1; s += 4) {
+        run(std::integral_constant<int, 0>{}, s);
+        if (s + 1 < s1) run(std::integral_constant<int, 4>{}, s + 1);
+        if (s + 2 < s1) run(std::integral_constant<int, 8>{}, s + 2);
+        if (s + 3 < s1) run(std::integral_constant<int, 12>{}, s + 3);
     }
     if (pend) {
 #pragma unroll
@@ -375,7 +424,8 @@ hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, 
 
 hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st) {
     const int nsteps = a.K / KS;
-    const int sps = (nsteps + splits - 1) / splits;
+    const int sps = ((nsteps + splits - 1) / splits + 3) & ~3;  // a multiple of 4 steps
+    if ((long)sps * (splits - 1) >= nsteps) return hipErrorInvalidValue;
     const dim3 grid((a.N + BNT - 1) / BNT, (a.M + BMT - 1) / BMT, splits);
     if (dtype == Q8_0)
         hipLaunchKernelGGL(mmqp_kernel<Q8_0>, grid, dim3(64 * NW), 0, st, a, sps);
