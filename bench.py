@@ -71,6 +71,9 @@ def parse():
     p.add_argument("--layout", choices=("packed", "gguf"), default="packed",
                    help="device weight layout of the headline value: aligned repack "
                         "(default) or GGUF bytes")
+    p.add_argument("--kernel-launch", choices=("graph", "stream"), default="graph",
+                   help="per_kernel timing: launches replayed from one HIP graph (default) "
+                        "or launched back to back from the host")
     p.add_argument("--graph", action="store_true",
                    help="replay each step as one captured HIP graph instead of four launches")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -337,10 +340,14 @@ class StepRunner:
         torch.cuda.synchronize()
         return t0.elapsed_time(t1) / steps
 
-    def time_kernels(self, launches, pool_bytes=512 << 20):
+    def time_kernels(self, launches, pool_bytes=512 << 20, graph=True):
         """Average launch time of each matrix alone: `launches` back-to-back
         launches rotating over >= pool_bytes of distinct copies of that matrix
-        (so every launch streams from HBM, not the Infinity Cache)."""
+        (so every launch streams from HBM, not the Infinity Cache).  With
+        `graph` the launches are captured in one HIP graph and replayed, so
+        the host's dispatch gaps between back-to-back launches (a few µs each)
+        are not counted as kernel time; events on the launch stream either
+        way."""
         import torch
         out = {}
         for i, (name, dt, N, K) in enumerate(CFG2):
@@ -354,13 +361,25 @@ class StepRunner:
             for c in copies:
                 self.launch(i, c)
             torch.cuda.synchronize()
+            g = None
+            if graph:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=self.side):
+                    for s in range(launches):
+                        self.launch(i, copies[s % len(copies)])
+                g.replay()  # warm
+                torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             with torch.cuda.stream(self.side):
                 e0.record()
-                for s in range(launches):
-                    self.launch(i, copies[s % len(copies)])
+                if g is not None:
+                    g.replay()
+                else:
+                    for s in range(launches):
+                        self.launch(i, copies[s % len(copies)])
                 e1.record()
             torch.cuda.synchronize()
+            del g
             us = e0.elapsed_time(e1) * 1e3 / launches
             b = alg_bytes(dt, N, K)
             out[name] = {"us": round(us, 2), "GBs": round(b / us / 1e3, 1),
@@ -428,7 +447,7 @@ def main():
             torch.cuda.synchronize()
             del src, dst
         ms = r.time_steps(args.steps, args.warmup, graph=args.graph)
-        kern = r.time_kernels(max(50, args.steps // 2))
+        kern = r.time_kernels(max(50, args.steps // 2), graph=args.kernel_launch == "graph")
         results[layout] = (ms, kern)
         r.free()
         del r
@@ -482,7 +501,8 @@ def main():
                    "launch": "hip_graph" if args.graph else "stream",
                    "step_alg_bytes": step_bytes,
                    "pct_hbm_peak": round(100 * value / PEAK_HBM_GBS, 1),
-                   "per_kernel": per_kernel},
+                   "per_kernel": per_kernel,
+                   "per_kernel_launch": "hip_graph" if args.kernel_launch == "graph" else "stream"},
         other: alt,
         "roofline": roofline,
         "cpu_baseline": cpu,
