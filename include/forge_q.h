@@ -206,7 +206,7 @@ int fq_ffn_down_residual_packed(uint32_t dtype, const float* x, const void* w_pa
  * reference: it is for callers that cannot allocate (code under HIP-graph
  * capture, serving loops and harnesses that forbid hipMalloc).  Returns
  * FQ_ERR_WORKSPACE when a call needs more than 64 MiB (for example M = 512 at
- * K = 4096 needs 42 MiB with 4 K-splits over 4096 rows).  All calls on one GPU
+ * K = N = 4096 needs 40-42 MiB with 4 K-splits).  All calls on one GPU
  * share the array: calls that overlap on one GPU (several streams or host
  * threads) race on it and must be serialised by the caller. */
 int fq_matmul_transB_noalloc(uint32_t dtype, const float* x, const void* w, const float* bias,
