@@ -166,18 +166,15 @@ __device__ __forceinline__ void codes16(const uint8_t* row, int g, uint32_t (&q)
     }
 }
 
-// Global memory straight into LDS: 16 or 4 bytes per lane, to lds + 16 lane
-// or lds + 4 lane (lds is wave-uniform, in M0).  Issued as inline assembly on
+// Global memory straight into LDS: 16 bytes per lane, to lds + 16 lane (lds
+// is wave-uniform, in M0).  Issued as inline assembly on
 // purpose: the compiler cannot tell which LDS bytes the builtin's copy
 // writes, so it waits for every outstanding load (vmcnt(0)) before the next
 // LDS read, which would serialise each step's loads with the step's compute.
-// The kernel counts the copies itself (wait_steps) before the barrier that
+// The kernel counts the copies itself (wait_step) before the barrier that
 // publishes them.
 __device__ __forceinline__ void dma16(const uint8_t* g, uint32_t lds) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(lds) : "memory");
-}
-__device__ __forceinline__ void dma4(const uint8_t* g, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(g), "{m0}"(lds) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void wait_vm() {
