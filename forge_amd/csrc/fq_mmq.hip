@@ -600,6 +600,37 @@ __global__ __launch_bounds__(64 * NWN * NWM) void mmq_kernel(MmqArgs a) {
 }
 
 // y = sum over splits of the partial slabs, in split order, plus the bias.
+// Four consecutive outputs per thread (16-byte loads and stores), the same
+// split order: bit-identical to reduce_kernel.  Needs M N and N multiples of
+// 4 and a 16-byte aligned y.
+__global__ __launch_bounds__(256) void reduce4_kernel(MmqArgs a, int splits) {
+    const size_t total = (size_t)a.M * a.N, t4 = total / 4;
+    const float4* part = reinterpret_cast<const float4*>(a.part);
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < t4; i += (size_t)gridDim.x * 256) {
+        float4 v = part[i];
+        for (int z = 1; z < splits; ++z) {
+            const float4 u = part[(size_t)z * t4 + i];
+            v.x += u.x;
+            v.y += u.y;
+            v.z += u.z;
+            v.w += u.w;
+        }
+        const int n = (int)((4 * i) % a.N);
+        if (a.bias_mode == 1) {
+            v.x += n < a.bias_len ? a.bias[n] : 0.0f;
+            v.y += n + 1 < a.bias_len ? a.bias[n + 1] : 0.0f;
+            v.z += n + 2 < a.bias_len ? a.bias[n + 2] : 0.0f;
+            v.w += n + 3 < a.bias_len ? a.bias[n + 3] : 0.0f;
+        } else if (a.bias_mode == 2) {
+            v.x += a.bias[4 * i];
+            v.y += a.bias[4 * i + 1];
+            v.z += a.bias[4 * i + 2];
+            v.w += a.bias[4 * i + 3];
+        }
+        reinterpret_cast<float4*>(a.y)[i] = v;
+    }
+}
+
 __global__ __launch_bounds__(256) void reduce_kernel(MmqArgs a, int splits) {
     const size_t total = (size_t)a.M * a.N;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
@@ -653,6 +684,13 @@ hipError_t launch_xprep(int dtype, const float* x, int M, int K, int NC, _Float1
 
 hipError_t launch_reduce(const MmqArgs& a, int splits, hipStream_t st) {
     const size_t total = (size_t)a.M * a.N;
+    if (a.N % 4 == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(a.part) & 15) == 0) {
+        const size_t t4 = total / 4;
+        const int grid = (int)((t4 + 255) / 256 < 4096 ? (t4 + 255) / 256 : 4096);
+        hipLaunchKernelGGL(reduce4_kernel, dim3(grid), dim3(256), 0, st, a, splits);
+        return hipGetLastError();
+    }
     const int grid = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
     hipLaunchKernelGGL(reduce_kernel, dim3(grid), dim3(256), 0, st, a, splits);
     return hipGetLastError();
@@ -664,10 +702,7 @@ hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, in
         return launch_f<decltype(f)::value>(a, shape, gx, gy, splits, st);
     });
     if (e != hipSuccess || splits <= 1) return e;
-    const size_t total = (size_t)a.M * a.N;
-    const int grid = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
-    hipLaunchKernelGGL(reduce_kernel, dim3(grid), dim3(256), 0, st, a, splits);
-    return hipGetLastError();
+    return launch_reduce(a, splits, st);
 }
 
 }  // namespace fq
