@@ -6,8 +6,8 @@
 // exact in fp16; one FMA per output and block folds in the block scale
 // (mmqp_kernel below).
 //
-// Token prep is two launches: the per-token exponent (one pass over x), then
-// the hi/lo operands in the A-operand layout (a second pass).
+// Token prep is one launch (xprep4_kernel): the per-token exponent, then the
+// hi/lo operands in the A-operand layout.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -30,66 +30,72 @@ constexpr int NBUF = 3;              // LDS buffers per operand: steps s, s + 1,
 constexpr int NW = 8;                // waves per work-group
 
 // ------------------------------------------------------------- token prep
-// One work-group per token: e = ilogb(max |x|) - 14 (0 for an all-zero
-// token), so that x 2^-e lies below 2^15 in magnitude.
-__global__ __launch_bounds__(256) void xexp_kernel(const float* __restrict__ x, int K,
-                                                   int* __restrict__ ex) {
-    __shared__ float wmax[4];
-    const int m = blockIdx.x;
-    const float* xr = x + (size_t)m * K;
-    float mx = 0.0f;
-#pragma unroll 4
-    for (int k = threadIdx.x * 4; k < K; k += 1024) {
-        const float4 v = *reinterpret_cast<const float4*>(xr + k);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-        ex[m] = (mx > 0.0f && mx <= 3.0e38f) ? ilogbf(mx) - 14 : 0;
-    }
-}
-
-// x 2^-e(token) split into fp16 hi + lo, written as the A operand of
-// v_mfma_f32_32x32x16_f16: for token tile T = m / 32 and quarter kq (the
-// MFMA half kq % 2 of block kq / 2), lane (m % 32) + 32 g holds elements
-// 32 (kq / 2) + 16 g + 8 (kq % 2) + slot_elem(j), j = 0..7, the hi block
-// then the lo block 512 halves on.  Work-group (step group,
-// T): wave w writes quarters 4 w .. 4 w + 3 of the group's 16, 2 KiB each,
-// contiguously.  Token slots past M are zero.
-constexpr int XG = 16;  // quarters (16 k each) per work-group
-__global__ __launch_bounds__(256) void xprep32_kernel(const float* __restrict__ x, int M, int K,
-                                                      const int* __restrict__ ex,
+// Per token an exponent e = ilogb(max |x|) - 14 (0 for an all-zero token),
+// so that x 2^-e lies below 2^15 in magnitude, and x 2^-e split into fp16
+// hi + lo, written as the A operand of v_mfma_f32_32x32x16_f16: for token
+// tile T = m / 32 and quarter kq (the MFMA half kq % 2 of block kq / 2), lane
+// (m % 32) + 32 g holds elements 32 (kq / 2) + 16 g + 8 (kq % 2) +
+// slot_elem(j), j = 0..7, the hi block then the lo block 512 halves on.
+//
+// One launch: work-group j owns tokens 4 j .. 4 j + 3 (all of
+// K).  Piece p = ((2 kq + g) 4 + t): token t's eight elements of quarter kq,
+// lane group g -- four consecutive threads write one 64-byte run (hi, and
+// lo 1 KiB on).  Pass 1 finds each token's largest |x| (x read once from
+// HBM), pass 2 reads the same bytes again (now from L2) and writes the
+// operands.  The work-groups cover every token slot of the last tile (slots
+// past M are zero).
+__global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ x, int M, int K,
+                                                      int* __restrict__ ex,
                                                       _Float16* __restrict__ xop) {
-    const int T = blockIdx.y, lane = threadIdx.x & 63;
-    const int lm = lane & 31, g = lane >> 5, m = 32 * T + lm;
-    const int kq0 = XG * blockIdx.x + 4 * (threadIdx.x >> 6);
-    const int e = m < M ? ex[m] : 0;
-    const float* src = x + (size_t)min(m, M - 1) * K + 16 * kq0 + 16 * g;
-    float4 v[8];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {  // kq0 is a multiple of 4: quarter kq0 + q
-        const float* sq = src + 32 * (q >> 1) + 8 * (q & 1);
-        v[2 * q] = *reinterpret_cast<const float4*>(sq);
-        v[2 * q + 1] = *reinterpret_cast<const float4*>(sq + 4);
+    __shared__ float wmax[16][4];
+    __shared__ int es[4];
+    const int tid = threadIdx.x, t = tid & 3;
+    const int m = 4 * blockIdx.x + t;
+    const bool live = m < M;
+    const float* xr = x + (size_t)min(m, M - 1) * K;
+    const int KQ = K / 16, P = 8 * KQ;  // pieces per work-group
+    auto src = [&](int p) {
+        const int gq = p >> 2, g = gq & 1, kq = gq >> 1;
+        return xr + 32 * (kq >> 1) + 16 * g + 8 * (kq & 1);
+    };
+    float mx = 0.0f;
+    for (int p = tid; p < P; p += 1024) {
+        const float* s = src(p);
+        const float4 a = *reinterpret_cast<const float4*>(s);
+        const float4 b = *reinterpret_cast<const float4*>(s + 4);
+        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                             fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float f[8] = {v[2 * q].x,     v[2 * q].y,     v[2 * q].z,     v[2 * q].w,
-                            v[2 * q + 1].x, v[2 * q + 1].y, v[2 * q + 1].z, v[2 * q + 1].w};
+    for (int o = 4; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((tid & 63) < 4) wmax[tid >> 6][t] = mx;
+    __syncthreads();
+    if (tid < 4) {
+        float v = 0.0f;
+        for (int w = 0; w < 16; ++w) v = fmaxf(v, wmax[w][tid]);
+        const int e = (v > 0.0f && v <= 3.0e38f) ? ilogbf(v) - 14 : 0;
+        es[tid] = e;
+        if (4 * blockIdx.x + tid < M) ex[4 * blockIdx.x + tid] = e;
+    }
+    __syncthreads();
+    const int e = es[t];
+    const int T = m >> 5, lm = m & 31;
+    for (int p = tid; p < P; p += 1024) {
+        const int gq = p >> 2, g = gq & 1, kq = gq >> 1;
         h8 hi = {}, lo = {};
-        if (m < M) {
+        if (live) {
+            const float* s = src(p);
+            const float4 a = *reinterpret_cast<const float4*>(s);
+            const float4 b = *reinterpret_cast<const float4*>(s + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float w = __builtin_amdgcn_ldexpf(f[slot_elem(j)], -e);
+                const float w = __builtin_amdgcn_ldexpf(v[slot_elem(j)], -e);
                 hi[j] = (_Float16)w;
                 lo[j] = (_Float16)(w - (float)hi[j]);
             }
         }
-        _Float16* dst = xop + ((size_t)T * (K / 16) + kq0 + q) * XT + lane * 8;
+        _Float16* dst = xop + ((size_t)T * KQ + kq) * XT + (lm + 32 * g) * 8;
         *reinterpret_cast<h8*>(dst) = hi;
         *reinterpret_cast<h8*>(dst + 512) = lo;
     }
@@ -114,7 +120,7 @@ struct PB;
 // The K order inside a 32-element block: MFMA half h takes from lane group g
 // the elements 16 g + 8 h + j, so a lane's 16 elements of a block are
 // contiguous (one 16-byte read of Q8_0 codes; the 16 Q4_0 bytes, low nibbles
-// for g = 0, high for g = 1).  xprep32_kernel lays the tokens out the same
+// for g = 0, high for g = 1).  xprep4_kernel lays the tokens out the same
 // way.
 //
 // Q8_0 block (34 B): d @0, qs int8[32] @2.  Lane group g: bytes
@@ -206,7 +212,7 @@ struct Tile {
 // Eight waves, each 64 tokens x 64 rows (2 x 2 tiles of 32 x 32).
 //
 // Per 32-element block b:
-//   A (32 tokens x 16 k): x 2^-e(token) as fp16 hi + lo (xprep32_kernel),
+//   A (32 tokens x 16 k): x 2^-e(token) as fp16 hi + lo (xprep4_kernel),
 //   B (16 k x 32 rows):   the block's integer codes, exact in fp16,
 //   D_b = A_hi B + A_lo B  (two MFMAs per 16 k, one fp32 result per block),
 //   acc += d_b(n) D_b      (one FMA per output and block),
@@ -410,12 +416,9 @@ int mmqp_tile_rows() { return BNT; }
 int mmqp_tile_tokens() { return BMT; }
 
 hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, hipStream_t st) {
-    if (K % (16 * XG) != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(xexp_kernel, dim3(M), dim3(256), 0, st, x, K, ex);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(xprep32_kernel, dim3(K / (16 * XG), (M + 31) / 32), dim3(256), 0, st, x,
-                       M, K, ex, xop);
+    if (K % 256 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(xprep4_kernel, dim3(8 * ((M + 31) / 32)), dim3(1024), 0, st, x, M, K, ex,
+                       xop);
     return hipGetLastError();
 }
 
