@@ -44,6 +44,18 @@ def test_shapes(dtype, M, N, K):
 
 
 @pytest.mark.parametrize("dtype", PREFILL)
+@pytest.mark.parametrize("M,N,K", [(64, 256, 1280), (100, 300, 2304), (512, 4096, 1280),
+                                   (130, 520, 256)])
+def test_split_k_ranges(dtype, M, N, K):
+    # K a multiple of 256 (the matrix-core prefill kernel): 20, 36, 20 and 4
+    # steps of 64, so the K-splits (each a multiple of four steps) come out
+    # at 5, 9, 3 (four rounded up to 8 steps each) and 1
+    w = synth.make_weights(dtype, N, K, seed=M + 7)
+    x = synth.make_x(M, K, seed=N + 3)
+    check(dtype, w, x, N, K, f"{F.fmt(dtype).name} split M={M} {N}x{K}")
+
+
+@pytest.mark.parametrize("dtype", PREFILL)
 def test_large_block_scales(dtype):
     # block scales up to the fp16 maximum in some rows (|q d| far outside the
     # fp16 range); one row mixes the largest scale with fp16 subnormal ones
