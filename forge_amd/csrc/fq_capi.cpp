@@ -169,6 +169,31 @@ MmqPlan plan_mmq(int M, int K, int N, int cus) {
     return p;
 }
 
+// Workspace bytes and K-splits of the Q8_0 / Q4_0 prefill kernel (M > 32,
+// K a multiple of 256): one work-group per CU and tile, K split while the
+// tiles leave CUs idle, each split a multiple of four 64-element steps.
+struct MmqpPlan {
+    int splits;
+    size_t xop_b, ex_b, part_b, total;
+};
+
+MmqpPlan plan_mmqp(int M, int K, int N, int cus) {
+    MmqpPlan p{};
+    const int Tn = (M + 31) / 32, nsteps = K / 64;
+    const int tn = fq::mmqp_tile_rows(), tm = fq::mmqp_tile_tokens();
+    const long tiles = (long)((N + tn - 1) / tn) * ((M + tm - 1) / tm);
+    int splits = tiles >= cus ? 1 : (int)std::min<long>(16, (cus + tiles - 1) / tiles);
+    splits = std::max(1, std::min(splits, nsteps / 4));
+    const int sps = ((nsteps + splits - 1) / splits + 3) & ~3;
+    p.splits = std::max(1, (nsteps + sps - 1) / sps);
+    p.xop_b = (size_t)Tn * K * 64 * 2;
+    p.ex_b = (size_t)M * 4;
+    p.part_b = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    p.total = 256 + al(p.xop_b) + al(p.ex_b) + al(p.part_b);
+    return p;
+}
+
 // M > 1 on the matrix cores: token operand preparation, then one tile per
 // work-group (K-split when the tiles alone do not fill the chip).  The
 // workspace is `fixed` (fixed_cap bytes) when given, else the stream's.
@@ -455,19 +480,10 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         // multiple of 256, 16-byte aligned weights): per-token operands, then
         // one work-group per CU and tile on v_mfma_f32_32x32x16_f16 (K-split
         // while the tiles leave CUs idle)
-        const int Tn = (M + 31) / 32, nsteps = K / 64;
-        const int tn = fq::mmqp_tile_rows(), tm = fq::mmqp_tile_tokens();
-        const long tiles = (long)((N + tn - 1) / tn) * ((M + tm - 1) / tm);
-        int splits = tiles >= di.cus ? 1 : (int)std::min<long>(16, (di.cus + tiles - 1) / tiles);
-        splits = std::max(1, std::min(splits, nsteps / 4));
-        {   // the kernel walks its K range four steps at a time
-            const int sps = ((nsteps + splits - 1) / splits + 3) & ~3;
-            splits = (nsteps + sps - 1) / sps;
-        }
+        const MmqpPlan pl = plan_mmqp(M, K, N, di.cus);
+        const int splits = pl.splits;
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-        const size_t xop_b = (size_t)Tn * K * 64 * 2, ex_b = (size_t)M * 4,
-                     part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;
-        const size_t need = 256 + al(xop_b) + al(ex_b) + al(part_b);
+        const size_t xop_b = pl.xop_b, ex_b = pl.ex_b, need = pl.total;
         std::unique_ptr<StreamScratch::Lease> lease;
         uint8_t* buf = fixed;
         if (fixed) {
@@ -840,6 +856,9 @@ int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
     // slabs grow with N, so N_max bounds them); slot 1: the fused ops' rows
     size_t need0 = 0;
     for (int m = 2; m <= M_max; ++m) need0 = std::max(need0, plan_mmq(m, K_max, N_max, di.cus).total);
+    if (K_max % 256 == 0)  // the Q8_0 / Q4_0 prefill kernel
+        for (int m = 33; m <= M_max; ++m)
+            need0 = std::max(need0, plan_mmqp(m, K_max, N_max, di.cus).total);
     const size_t need1 = 2 * (size_t)M_max * N_max * sizeof(float);
     uint8_t* p = nullptr;
     if (need0) {
