@@ -853,12 +853,17 @@ int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
     if (e != hipSuccess) return hip_fail(e);
     const DevInfo di = device_info(dev);
     // slot 0: the largest MFMA-path plan for up to M_max tokens (the split-K
-    // slabs grow with N, so N_max bounds them); slot 1: the fused ops' rows
+    // slabs grow with splits x N, and fewer rows can mean more splits: every
+    // row count that changes the tile count is tried, with K_max and, for the
+    // Q8_0 / Q4_0 prefill kernel, the largest multiple of 256 up to K_max)
     size_t need0 = 0;
-    for (int m = 2; m <= M_max; ++m) need0 = std::max(need0, plan_mmq(m, K_max, N_max, di.cus).total);
-    if (K_max % 256 == 0)  // the Q8_0 / Q4_0 prefill kernel
-        for (int m = 33; m <= M_max; ++m)
-            need0 = std::max(need0, plan_mmqp(m, K_max, N_max, di.cus).total);
+    const int Kp = K_max - K_max % 256;
+    for (int n = N_max; n > 0; n = n > 128 ? ((n - 1) / 128) * 128 : 0) {
+        for (int m = 2; m <= M_max; ++m) {
+            need0 = std::max(need0, plan_mmq(m, K_max, n, di.cus).total);
+            if (m > 32 && Kp > 0) need0 = std::max(need0, plan_mmqp(m, Kp, n, di.cus).total);
+        }
+    }
     const size_t need1 = 2 * (size_t)M_max * N_max * sizeof(float);
     uint8_t* p = nullptr;
     if (need0) {
