@@ -170,8 +170,9 @@ MmqPlan plan_mmq(int M, int K, int N, int cus) {
 }
 
 // Workspace bytes and K-splits of the Q8_0 / Q4_0 prefill kernel (M > 32,
-// K a multiple of 256): one work-group per CU and tile, K split while the
-// tiles leave CUs idle, each split a multiple of four 64-element steps.
+// K a multiple of 256): one work-group per CU and tile, K split when that
+// shortens the busiest CU's work, each split a multiple of four 64-element
+// steps.
 struct MmqpPlan {
     int splits;
     size_t xop_b, ex_b, part_b, total;
@@ -182,10 +183,23 @@ MmqpPlan plan_mmqp(int M, int K, int N, int cus) {
     const int Tn = (M + 31) / 32, nsteps = K / 64;
     const int tn = fq::mmqp_tile_rows(), tm = fq::mmqp_tile_tokens();
     const long tiles = (long)((N + tn - 1) / tn) * ((M + tm - 1) / tm);
-    int splits = tiles >= cus ? 1 : (int)std::min<long>(16, (cus + tiles - 1) / tiles);
-    splits = std::max(1, std::min(splits, nsteps / 4));
-    const int sps = ((nsteps + splits - 1) / splits + 3) & ~3;
-    p.splits = std::max(1, (nsteps + sps - 1) / sps);
+    // the split count with the fewest steps on the busiest CU (rounds of
+    // work-groups x steps per split), taken only when it saves at least a
+    // quarter of the unsplit count: every split adds a partial slab and its
+    // share of the reduce (14336 x 4096 x 512: 224 tiles run fastest
+    // unsplit, 4096 x 4096 x 512: 64 tiles with 4 splits)
+    const long cost1 = ((tiles + cus - 1) / cus) * nsteps;
+    long best = cost1;
+    p.splits = 1;
+    for (int sp = 2; sp <= std::min(16, nsteps / 4); ++sp) {
+        const int sps = ((nsteps + sp - 1) / sp + 3) & ~3;
+        const int eff = (nsteps + sps - 1) / sps;  // non-empty splits
+        const long cost = ((tiles * eff + cus - 1) / cus) * sps;
+        if (4 * cost <= 3 * cost1 && cost < best) {
+            best = cost;
+            p.splits = eff;
+        }
+    }
     p.xop_b = (size_t)Tn * K * 64 * 2;
     p.ex_b = (size_t)M * 4;
     p.part_b = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
