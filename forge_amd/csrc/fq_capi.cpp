@@ -175,7 +175,7 @@ MmqPlan plan_mmq(int M, int K, int N, int cus) {
 // steps.
 struct MmqpPlan {
     int splits;
-    size_t xop_b, ex_b, part_b, total;
+    size_t xop_b, ex_b, sum_b, part_b, total;
 };
 
 MmqpPlan plan_mmqp(int M, int K, int N, int cus) {
@@ -202,9 +202,10 @@ MmqpPlan plan_mmqp(int M, int K, int N, int cus) {
     }
     p.xop_b = (size_t)Tn * K * 64 * 2;
     p.ex_b = (size_t)M * 4;
+    p.sum_b = (size_t)Tn * 32 * K / 32 * 4;  // sub-block sums (formats with a min term)
     p.part_b = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    p.total = 256 + al(p.xop_b) + al(p.ex_b) + al(p.part_b);
+    p.total = 256 + al(p.xop_b) + al(p.ex_b) + al(p.sum_b) + al(p.part_b);
     return p;
 }
 
@@ -490,14 +491,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
 
     if (fq::mmqp_supported((int)dtype) && M > 32 && K > 0 && K % 256 == 0 &&
         (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
-        // prefill, Q8_0 / Q4_0 rows that are whole 16-byte chunks (K a
-        // multiple of 256, 16-byte aligned weights): per-token operands, then
+        // prefill, Q8_0 / Q4_0 / Q4_K rows that are whole 16-byte chunks (K
+        // a multiple of 256, 16-byte aligned weights): per-token operands, then
         // one work-group per CU and tile on v_mfma_f32_32x32x16_f16 (K-split
         // while the tiles leave CUs idle)
         const MmqpPlan pl = plan_mmqp(M, K, N, di.cus);
         const int splits = pl.splits;
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-        const size_t xop_b = pl.xop_b, ex_b = pl.ex_b, need = pl.total;
+        const size_t xop_b = pl.xop_b, ex_b = pl.ex_b, sum_b = pl.sum_b, need = pl.total;
         std::unique_ptr<StreamScratch::Lease> lease;
         uint8_t* buf = fixed;
         if (fixed) {
@@ -511,7 +512,10 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         a.w = static_cast<const uint8_t*>(w);
         a.xop = buf;
         a.ex = reinterpret_cast<const int*>(buf + al(xop_b));
-        a.part = splits > 1 ? reinterpret_cast<float*>(buf + al(xop_b) + al(ex_b)) : nullptr;
+        a.xsum = dtype == FQ_DTYPE_Q4_K ? reinterpret_cast<const float*>(buf + al(xop_b) + al(ex_b))
+                               : nullptr;
+        a.part = splits > 1 ? reinterpret_cast<float*>(buf + al(xop_b) + al(ex_b) + al(sum_b))
+                            : nullptr;
         a.y = y;
         a.bias = bias;
         a.bias_len = bias_mode ? bias_len : 0;
@@ -521,7 +525,7 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         a.K = K;
         a.row_bytes = (K / g.be) * g.bb;
         e = fq::launch_xprep32(x, M, K, reinterpret_cast<_Float16*>(buf),
-                               const_cast<int*>(a.ex), st);
+                               const_cast<int*>(a.ex), const_cast<float*>(a.xsum), st);
         if (e != hipSuccess) return hip_fail(e);
         e = fq::launch_mmqp((int)dtype, a, splits, st);
         if (e == hipSuccess && splits > 1) e = fq::launch_reduce(a, splits, st);

@@ -87,7 +87,8 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hip
 bool mmqp_supported(int dtype);
 int mmqp_tile_rows();    // rows per work-group tile
 int mmqp_tile_tokens();  // tokens per work-group tile
-hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, hipStream_t st);
+hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, float* xsum,
+                          hipStream_t st);
 hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st);
 hipError_t launch_reduce(const MmqArgs& a, int splits, hipStream_t st);
 hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,

@@ -46,7 +46,8 @@ constexpr int NW = 8;                // waves per work-group
 // past M are zero).
 __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ x, int M, int K,
                                                       int* __restrict__ ex,
-                                                      _Float16* __restrict__ xop) {
+                                                      _Float16* __restrict__ xop,
+                                                      float* __restrict__ xsum) {
     __shared__ float wmax[16][4];
     __shared__ int es[4];
     const int tid = threadIdx.x, t = tid & 3;
@@ -80,24 +81,35 @@ __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ 
     __syncthreads();
     const int e = es[t];
     const int T = m >> 5, lm = m & 31;
-    for (int p = tid; p < P; p += 1024) {
+    for (int p = tid; p < P; p += 1024) {  // P is a multiple of 64: whole waves
         const int gq = p >> 2, g = gq & 1, kq = gq >> 1;
         h8 hi = {}, lo = {};
+        float w[8] = {};
         if (live) {
             const float* s = src(p);
             const float4 a = *reinterpret_cast<const float4*>(s);
             const float4 b = *reinterpret_cast<const float4*>(s + 4);
             const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
+            for (int j = 0; j < 8; ++j) w[j] = __builtin_amdgcn_ldexpf(v[j], -e);
+#pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float w = __builtin_amdgcn_ldexpf(v[slot_elem(j)], -e);
-                hi[j] = (_Float16)w;
-                lo[j] = (_Float16)(w - (float)hi[j]);
+                const float u = w[slot_elem(j)];
+                hi[j] = (_Float16)u;
+                lo[j] = (_Float16)(u - (float)hi[j]);
             }
         }
         _Float16* dst = xop + ((size_t)T * KQ + kq) * XT + (lm + 32 * g) * 8;
         *reinterpret_cast<h8*>(dst) = hi;
         *reinterpret_cast<h8*>(dst + 512) = lo;
+        if (xsum) {
+            // the token's sum of x 2^-e over its 32-element sub-block kq / 2:
+            // pieces p, p ^ 4, p ^ 8, p ^ 12 of one wave, added in a fixed tree
+            float t8 = ((w[0] + w[1]) + (w[2] + w[3])) + ((w[4] + w[5]) + (w[6] + w[7]));
+            t8 += __shfl_xor(t8, 4, 64);
+            t8 += __shfl_xor(t8, 8, 64);
+            if ((p & 12) == 0) xsum[((size_t)T * (K / 32) + (kq >> 1)) * 32 + lm] = t8;
+        }
     }
 }
 
@@ -130,6 +142,8 @@ template <>
 struct PB<Q8_0> {
     static constexpr int BB = 34, SB = 2 * BB;  // bytes per block, per step
     static constexpr int GS = 16;               // byte offset of lane group g
+    static constexpr bool MIN = false;          // no per-block minimum term
+    template <int B>
     __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
         b0 = perm8(q[0] ^ 0x80808080u, q[1] ^ 0x80808080u, (_Float16)1152.0f);
         b1 = perm8(q[2] ^ 0x80808080u, q[3] ^ 0x80808080u, (_Float16)1152.0f);
@@ -143,9 +157,48 @@ template <>
 struct PB<Q4_0> {
     static constexpr int BB = 18, SB = 2 * BB;
     static constexpr int GS = 0;
+    static constexpr bool MIN = false;
+    template <int B>
     __device__ static void ops(const uint32_t (&q)[4], int g, h8& b0, h8& b1) {
         b0 = nib8(q[0], q[1], 4 * g, (_Float16)1032.0f);
         b1 = nib8(q[2], q[3], 4 * g, (_Float16)1032.0f);
+    }
+};
+
+// Q4_K super-block (144 B, matmul.cpp:340-377): d @0, dmin @2, scales[12]
+// @4 (6-bit scale and min per 32-element sub-block), qs[128] @16.  A step
+// (64 elements) is sub-block pair p = s mod 4 of super-block s / 4: the
+// low nibbles of qs[32 p, 32 p + 32) are sub-block 2 p (block b = 0), the
+// high nibbles sub-block 2 p + 1 (b = 1).  Per row and step three 16-byte
+// chunks are copied, all aligned: the header and the pair's 32 code bytes.
+// Lane group g: bytes 16 g .. 16 g + 15 of the pair, nibble b; half h =
+// bytes 8 h .. 8 h + 7.  w = d sc q - dmin m: the min term goes through
+// the per-token sub-block sums of xprep4_kernel.
+template <>
+struct PB<Q4_K> {
+    static constexpr int CH = 3;
+    static constexpr bool MIN = true;
+    template <int B>
+    __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
+        b0 = nib8(q[0], q[1], 4 * B, (_Float16)1024.0f);
+        b1 = nib8(q[2], q[3], 4 * B, (_Float16)1024.0f);
+    }
+};
+
+// Chunks per row and step, and the byte offset (within the row) of chunk p
+// of step s, less 16 p.  Q8_0 / Q4_0: a step of a row (68 / 36 bytes)
+// starts (s SB) mod 16 = 0, 4, 8 or 12 bytes into a 16-byte chunk (rows are
+// 16-byte aligned), so CH chunks cover it for every step.
+template <int F>
+struct Chunks {
+    static constexpr int CH = (PB<F>::SB + 12 + 15) / 16;
+    __device__ static size_t off(int s, int) { return (size_t)s * PB<F>::SB & ~(size_t)15; }
+};
+template <>
+struct Chunks<Q4_K> {
+    static constexpr int CH = 3;
+    __device__ static size_t off(int s, int p) {
+        return (size_t)144 * (s >> 2) + (p ? 32 * (s & 3) : 0);
     }
 };
 
@@ -172,6 +225,38 @@ __device__ __forceinline__ void codes16(const uint8_t* row, int g, uint32_t (&q)
     }
 }
 
+// The 16 code bytes of lane group g of block B and the block's scale and
+// minimum coefficient (d sc, dmin m; the minimum is 0 without a min term),
+// for a row slot whose step starts O4 bytes into its first chunk.
+template <int F, int O4, int B>
+__device__ __forceinline__ void codes(const uint8_t* row, int g, uint32_t (&q)[4]) {
+    if constexpr (F == Q4_K) {  // planes of BNT x 16 bytes: header, codes 0..15, codes 16..31
+        typedef const __attribute__((address_space(3))) fq_u32x4* lds_v4;
+        const fq_u32x4 v =
+            *reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(row + BNT * 16 * (1 + g)));
+        q[0] = v[0];
+        q[1] = v[1];
+        q[2] = v[2];
+        q[3] = v[3];
+    } else {
+        codes16<F, O4, B>(row, g, q);
+    }
+}
+template <int F, int O4, int B>
+__device__ __forceinline__ void scales(const uint8_t* row, float& db, float& mn) {
+    if constexpr (F == Q4_K) {
+        typedef const __attribute__((address_space(3))) fq_u32x4* lds_v4;
+        const fq_u32x4 h = *reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(row));
+        uint32_t sa, ma, sb, mb;
+        Fmt<Q4_K>::scale_min(uint4{h[0], h[1], h[2], h[3]}, O4 / 4, sa, ma, sb, mb);
+        db = f16_hw(h[0] & 0xFFFFu) * (float)(B ? sb : sa);
+        mn = f16_hw(h[0] >> 16) * (float)(B ? mb : ma);
+    } else {
+        db = f16_hw(*reinterpret_cast<const uint16_t*>(row + O4 + PB<F>::BB * B));
+        mn = 0.0f;
+    }
+}
+
 // Global memory straight into LDS: 16 bytes per lane, to lds + 16 lane (lds
 // is wave-uniform, in M0).  Issued as inline assembly on
 // purpose: the compiler cannot tell which LDS bytes the builtin's copy
@@ -190,20 +275,22 @@ __device__ __forceinline__ void wait_vm() {
 
 template <int F>
 struct Tile {
-    using P = PB<F>;
-    // A step of a row (68 / 36 bytes) starts (s SB) mod 16 = 0, 4, 8 or 12
-    // bytes into a 16-byte chunk (rows are 16-byte aligned), so CH chunks
-    // cover it for every step.
-    static constexpr int CH = (P::SB + 12 + 15) / 16;   // chunks per row and step
-    static constexpr int WROW = 16 * CH;                // LDS bytes per weight row and step
+    static constexpr int CH = Chunks<F>::CH;            // chunks per row and step
+    // Q8_0 / Q4_0: rows of CH chunks; Q4_K: CH planes of one chunk per row
+    static constexpr bool PLANES = F == Q4_K;
+    static constexpr int WROW = PLANES ? 16 : 16 * CH;  // LDS bytes between rows
     static constexpr int WCH = BNT * CH;                // chunks of a step's weight tile
     static constexpr int WIN = WCH / 64;                // copy instructions per step (whole)
     static_assert(WCH % 64 == 0, "whole copy instructions");
     static constexpr int WI_LO = WIN / NW, WI_HI = (WIN + NW - 1) / NW;
     static constexpr int W_HI = WIN - NW * WI_LO;       // waves that issue WI_HI copies
-    static constexpr int WBUF = BNT * WROW;             // bytes per weight buffer
-    static constexpr int XI = 4;                        // token copies per wave (1 KiB each)
-    static constexpr int XBUF = 16 * XT * 2;            // bytes per token buffer
+    static constexpr int WBUF = BNT * 16 * CH;          // bytes per weight buffer
+    static constexpr bool MIN = PB<F>::MIN;
+    // token copies per wave: 1 KiB each, plus one of 128 bytes (8 lanes) of
+    // sub-block sums with a min term
+    static constexpr int XI = 4 + (MIN ? 1 : 0);
+    static constexpr int XOPB = 16 * XT * 2;            // token operand bytes per buffer
+    static constexpr int XBUF = XOPB + (MIN ? 1024 : 0);
     static constexpr int LDS = NBUF * (XBUF + WBUF);
 };
 
@@ -252,9 +339,15 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
 #pragma unroll
     for (int q = 0; q < TL::WI_HI; ++q) {
         const int L = min(64 * (NW * q + wave) + lane, TL::WCH - 1);
-        const int r = L / TL::CH, p = L - r * TL::CH;
+        // row-major [row][CH] slots, or (PLANES) chunk-major [CH][row]: copy
+        // instruction k = NW q + wave is plane k / 4, wave-uniform
+        const int r = TL::PLANES ? L % BNT : L / TL::CH;
+        const int p = TL::PLANES ? L / BNT : L - r * TL::CH;
         wsrc[q] = a.w + (size_t)min(n0 + r, a.N - 1) * a.row_bytes + 16 * p;
     }
+    // sub-block sums (min term): tile T, block wave & 1, lanes 0..7
+    const float* ssrc = TL::MIN ? a.xsum + ((size_t)T * (a.K / 32) + (wave & 1)) * 32 + 4 * lane
+                                : nullptr;
     const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds);
     auto issue = [&](int s) {
@@ -262,12 +355,17 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
         const uint32_t xl = lds_base + buf * TL::XBUF + wave * 4096;
         const uint8_t* xg = xsrc + (size_t)s * 4 * XT * 2;
 #pragma unroll
-        for (int i = 0; i < TL::XI; ++i) dma16(xg + 1024 * i, xl + 1024 * i);
+        for (int i = 0; i < 4; ++i) dma16(xg + 1024 * i, xl + 1024 * i);
+        if constexpr (TL::MIN) {
+            const uint32_t sl = lds_base + buf * TL::XBUF + TL::XOPB + wave * 128;
+            if (lane < 8) dma16(reinterpret_cast<const uint8_t*>(ssrc + (size_t)64 * s), sl);
+        }
         const uint32_t wl = lds_base + NBUF * TL::XBUF + buf * TL::WBUF + wave * 1024;
-        const size_t koff = (size_t)s * P::SB & ~(size_t)15;
 #pragma unroll
         for (int q = 0; q < TL::WI_HI; ++q)
-            if (q < nwi) dma16(wsrc[q] + koff, wl + NW * 1024 * q);
+            if (q < nwi)
+                dma16(wsrc[q] + Chunks<F>::off(s, TL::PLANES ? (NW * q + wave) >> 2 : 0),
+                      wl + NW * 1024 * q);
     };
     // this wave's copies of step s are complete (those of step s + 1 may
     // still be in flight)
@@ -303,6 +401,7 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
     bool pend = false;
     auto step = [&](auto o4, const _Float16* xs, const uint8_t* ws) {
         constexpr int O4 = decltype(o4)::value;
+        float mn[2][2];  // dmin m of row tile j, block b (0 without a min term)
         h8 A[2][4];
         read_a(xs, 0, 0, A[0]);
 #pragma unroll
@@ -314,10 +413,15 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
             for (int j = 0; j < 2; ++j) {
                 const uint8_t* row = ws + (64 * wn + 32 * j + c) * WROW;
                 uint32_t q[4];
-                if (b == 0) codes16<F, O4, 0>(row, g, q);
-                else codes16<F, O4, 1>(row, g, q);
-                P::ops(q, g, B[j][0], B[j][1]);
-                db[j] = f16_hw(*reinterpret_cast<const uint16_t*>(row + O4 + P::BB * b));
+                if (b == 0) {
+                    codes<F, O4, 0>(row, g, q);
+                    P::template ops<0>(q, g, B[j][0], B[j][1]);
+                    scales<F, O4, 0>(row, db[j], mn[j][0]);
+                } else {
+                    codes<F, O4, 1>(row, g, q);
+                    P::template ops<1>(q, g, B[j][0], B[j][1]);
+                    scales<F, O4, 1>(row, db[j], mn[j][1]);
+                }
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -351,6 +455,22 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
                 dbp[0] = db[0];
                 dbp[1] = db[1];
                 pend = true;
+            }
+        }
+        if constexpr (TL::MIN) {
+            // acc -= S (token) x dmin m (row) over the step's two sub-blocks:
+            // one v_mfma_f32_32x32x2_f32 per tile (K = the two sub-blocks),
+            // A = lane (c, g): the scaled sum of token c over block g, B =
+            // -dmin m of row c of the row tile for block g
+            const float* sv = reinterpret_cast<const float*>(
+                reinterpret_cast<const uint8_t*>(xs) + TL::XOPB);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float sa = sv[((2 * wm + i) * 2 + g) * 32 + c];
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                        sa, -(g ? mn[j][1] : mn[j][0]), acc[i][j], 0, 0, 0);
             }
         }
     };
@@ -411,14 +531,15 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
 
 }  // namespace
 
-bool mmqp_supported(int dtype) { return dtype == Q8_0 || dtype == Q4_0; }
+bool mmqp_supported(int dtype) { return dtype == Q8_0 || dtype == Q4_0 || dtype == Q4_K; }
 int mmqp_tile_rows() { return BNT; }
 int mmqp_tile_tokens() { return BMT; }
 
-hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, hipStream_t st) {
+hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, float* xsum,
+                          hipStream_t st) {
     if (K % 256 != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(xprep4_kernel, dim3(8 * ((M + 31) / 32)), dim3(1024), 0, st, x, M, K, ex,
-                       xop);
+                       xop, xsum);
     return hipGetLastError();
 }
 
@@ -431,6 +552,8 @@ hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st) 
         hipLaunchKernelGGL(mmqp_kernel<Q8_0>, grid, dim3(64 * NW), 0, st, a, sps);
     else if (dtype == Q4_0)
         hipLaunchKernelGGL(mmqp_kernel<Q4_0>, grid, dim3(64 * NW), 0, st, a, sps);
+    else if (dtype == Q4_K)
+        hipLaunchKernelGGL(mmqp_kernel<Q4_K>, grid, dim3(64 * NW), 0, st, a, sps);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

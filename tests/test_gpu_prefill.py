@@ -1,7 +1,8 @@
-"""GPU parity of the prefill path (M > 32, fq_mmq.hip) against the oracle.
+"""GPU parity of the prefill path (M > 32: fq_mmqp.hip when K is a multiple
+of 256, else fq_mmq.hip) against the oracle.
 
 Edge cases beyond the token-count and format sweeps of test_gpu_mmq.py, for
-the two prefill formats of the benchmark (Q8_0, Q4_0): N and M tails with
+the two prefill formats of the benchmark (Q8_0, Q4_0) and Q4_K: N and M tails with
 one row and one block of K, block scales up to the fp16 maximum (and fp16
 subnormal ones in the same row), activations spanning 60 decades inside one
 token, bias modes, determinism, and an activation pointer that is only
@@ -21,7 +22,7 @@ from test_gpu_parity import dev_weight, run
 
 pytestmark = pytest.mark.gpu
 
-PREFILL = [F.Q8_0, F.Q4_0]
+PREFILL = [F.Q8_0, F.Q4_0, F.Q4_K]
 
 
 def check(dtype, w, x, N, K, what, bias=None):
@@ -38,6 +39,8 @@ def check(dtype, w, x, N, K, what, bias=None):
 @pytest.mark.parametrize("M,N,K", [(33, 1, 32), (40, 129, 4096), (64, 1024, 2048),
                                    (100, 333, 1024), (200, 2048, 512), (65, 16, 18944)])
 def test_shapes(dtype, M, N, K):
+    if K % F.fmt(dtype).block_elems:
+        pytest.skip("K is not a whole number of super-blocks")
     w = synth.make_weights(dtype, N, K, seed=M + N)
     x = synth.make_x(M, K, seed=K + M)
     check(dtype, w, x, N, K, f"{F.fmt(dtype).name} M={M} {N}x{K}")
@@ -61,12 +64,13 @@ def test_large_block_scales(dtype):
     # fp16 range); one row mixes the largest scale with fp16 subnormal ones
     M, N, K = 48, 256, 2048
     f = F.fmt(dtype)
-    w = synth.make_weights(dtype, N, K, seed=21).reshape(N, K // 32, f.block_bytes)
+    nb = K // f.block_elems
+    w = synth.make_weights(dtype, N, K, seed=21).reshape(N, nb, f.block_bytes)
     rng = np.random.default_rng(22)
     big = np.array([300.0, 4000.0, 65504.0, -20000.0], np.float16)
     for r in (0, 5, 130, 255):
-        cols = rng.choice(K // 32, size=8, replace=False)
-        w[r, cols, 0:2] = rng.choice(big, size=8).view(np.uint8).reshape(8, 2)
+        cols = rng.choice(nb, size=min(8, nb), replace=False)
+        w[r, cols, 0:2] = rng.choice(big, size=len(cols)).view(np.uint8).reshape(len(cols), 2)
     w[77, :, 0:2] = np.array([1e-7], np.float16).view(np.uint8)  # subnormal
     w[77, 3, 0:2] = np.array([65504.0], np.float16).view(np.uint8)
     w[200, :, 0:2] = np.array([1000.0], np.float16).view(np.uint8)  # a whole row
