@@ -142,6 +142,7 @@ template <>
 struct PB<Q8_0> {
     static constexpr int BB = 34, SB = 2 * BB;  // bytes per block, per step
     static constexpr int GS = 16;               // byte offset of lane group g
+    static constexpr int QOFF = 2;              // codes after the scale
     static constexpr bool MIN = false;          // no per-block minimum term
     template <int B>
     __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
@@ -157,11 +158,27 @@ template <>
 struct PB<Q4_0> {
     static constexpr int BB = 18, SB = 2 * BB;
     static constexpr int GS = 0;
+    static constexpr int QOFF = 2;
     static constexpr bool MIN = false;
     template <int B>
     __device__ static void ops(const uint32_t (&q)[4], int g, h8& b0, h8& b1) {
         b0 = nib8(q[0], q[1], 4 * g, (_Float16)1032.0f);
         b1 = nib8(q[2], q[3], 4 * g, (_Float16)1032.0f);
+    }
+};
+
+// Q4_1 block (20 B): d @0, m @2, qs[16] @4 as Q4_0 but unsigned, w = d q +
+// m: the m term goes through the per-token block sums of xprep4_kernel.
+template <>
+struct PB<Q4_1> {
+    static constexpr int BB = 20, SB = 2 * BB;
+    static constexpr int GS = 0;
+    static constexpr int QOFF = 4;
+    static constexpr bool MIN = true;
+    template <int B>
+    __device__ static void ops(const uint32_t (&q)[4], int g, h8& b0, h8& b1) {
+        b0 = nib8(q[0], q[1], 4 * g, (_Float16)1024.0f);
+        b1 = nib8(q[2], q[3], 4 * g, (_Float16)1024.0f);
     }
 };
 
@@ -192,11 +209,21 @@ struct PB<Q4_K> {
 template <int F>
 struct Chunks {
     static constexpr int CH = (PB<F>::SB + 12 + 15) / 16;
+    // step s0 + u starts (u SB) mod 16 bytes into its first chunk (s0 a
+    // multiple of 4 and rows 16-byte aligned)
+    static constexpr int o4(int u) { return u * PB<F>::SB & 15; }
     __device__ static size_t off(int s, int) { return (size_t)s * PB<F>::SB & ~(size_t)15; }
+};
+template <>
+struct Chunks<Q4_1> {  // a step (40 bytes) starts 0 or 8 bytes into a chunk
+    static constexpr int CH = 3;
+    static constexpr int o4(int u) { return u * 40 & 15; }
+    __device__ static size_t off(int s, int) { return (size_t)s * 40 & ~(size_t)15; }
 };
 template <>
 struct Chunks<Q4_K> {
     static constexpr int CH = 3;
+    static constexpr int o4(int u) { return 4 * u; }  // the pair index, as 4 p
     __device__ static size_t off(int s, int p) {
         return (size_t)144 * (s >> 2) + (p ? 32 * (s & 3) : 0);
     }
@@ -210,7 +237,7 @@ struct Chunks<Q4_K> {
 template <int F, int O4, int B>
 __device__ __forceinline__ void codes16(const uint8_t* row, int g, uint32_t (&q)[4]) {
     using P = PB<F>;
-    constexpr int X = O4 + P::BB * B + 2;  // first code byte, lane group 0
+    constexpr int X = O4 + P::BB * B + P::QOFF;  // first code byte, lane group 0
     constexpr int SH = X & 15, SD = SH >> 2, R = SH & 3;
     const uint8_t* c0 = row + (X & ~15) + P::GS * g;
     typedef const __attribute__((address_space(3))) fq_u32x4* lds_v4;
@@ -251,6 +278,10 @@ __device__ __forceinline__ void scales(const uint8_t* row, float& db, float& mn)
         Fmt<Q4_K>::scale_min(uint4{h[0], h[1], h[2], h[3]}, O4 / 4, sa, ma, sb, mb);
         db = f16_hw(h[0] & 0xFFFFu) * (float)(B ? sb : sa);
         mn = f16_hw(h[0] >> 16) * (float)(B ? mb : ma);
+    } else if constexpr (F == Q4_1) {
+        const uint32_t dm = lds4_a2(row + O4 + PB<F>::BB * B);
+        db = f16_hw(dm & 0xFFFFu);
+        mn = -f16_hw(dm >> 16);  // w = d q + m: the term is -(-m) S
     } else {
         db = f16_hw(*reinterpret_cast<const uint16_t*>(row + O4 + PB<F>::BB * B));
         mn = 0.0f;
@@ -490,10 +521,10 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
     // are 4 mod 16; s0 is a multiple of 4), so four steps per iteration
     // give every read a constant offset
     for (int s = s0; s < s1; s += 4) {
-        run(std::integral_constant<int, 0>{}, s);
-        if (s + 1 < s1) run(std::integral_constant<int, 4>{}, s + 1);
-        if (s + 2 < s1) run(std::integral_constant<int, 8>{}, s + 2);
-        if (s + 3 < s1) run(std::integral_constant<int, 12>{}, s + 3);
+        run(std::integral_constant<int, Chunks<F>::o4(0)>{}, s);
+        if (s + 1 < s1) run(std::integral_constant<int, Chunks<F>::o4(1)>{}, s + 1);
+        if (s + 2 < s1) run(std::integral_constant<int, Chunks<F>::o4(2)>{}, s + 2);
+        if (s + 3 < s1) run(std::integral_constant<int, Chunks<F>::o4(3)>{}, s + 3);
     }
     if (pend) {
 #pragma unroll
@@ -531,7 +562,9 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
 
 }  // namespace
 
-bool mmqp_supported(int dtype) { return dtype == Q8_0 || dtype == Q4_0 || dtype == Q4_K; }
+bool mmqp_supported(int dtype) {
+    return dtype == Q8_0 || dtype == Q4_0 || dtype == Q4_1 || dtype == Q4_K;
+}
 int mmqp_tile_rows() { return BNT; }
 int mmqp_tile_tokens() { return BMT; }
 
@@ -552,6 +585,8 @@ hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st) 
         hipLaunchKernelGGL(mmqp_kernel<Q8_0>, grid, dim3(64 * NW), 0, st, a, sps);
     else if (dtype == Q4_0)
         hipLaunchKernelGGL(mmqp_kernel<Q4_0>, grid, dim3(64 * NW), 0, st, a, sps);
+    else if (dtype == Q4_1)
+        hipLaunchKernelGGL(mmqp_kernel<Q4_1>, grid, dim3(64 * NW), 0, st, a, sps);
     else if (dtype == Q4_K)
         hipLaunchKernelGGL(mmqp_kernel<Q4_K>, grid, dim3(64 * NW), 0, st, a, sps);
     else

@@ -2,7 +2,7 @@
 of 256, else fq_mmq.hip) against the oracle.
 
 Edge cases beyond the token-count and format sweeps of test_gpu_mmq.py, for
-the two prefill formats of the benchmark (Q8_0, Q4_0) and Q4_K: N and M tails with
+the two prefill formats of the benchmark (Q8_0, Q4_0), Q4_1 and Q4_K: N and M tails with
 one row and one block of K, block scales up to the fp16 maximum (and fp16
 subnormal ones in the same row), activations spanning 60 decades inside one
 token, bias modes, determinism, and an activation pointer that is only
@@ -22,7 +22,7 @@ from test_gpu_parity import dev_weight, run
 
 pytestmark = pytest.mark.gpu
 
-PREFILL = [F.Q8_0, F.Q4_0, F.Q4_K]
+PREFILL = [F.Q8_0, F.Q4_0, F.Q4_1, F.Q4_K]
 
 
 def check(dtype, w, x, N, K, what, bias=None):
