@@ -41,9 +41,9 @@ constexpr int NW = 8;                // waves per work-group
 // K).  Piece p = ((2 kq + g) 4 + t): token t's eight elements of quarter kq,
 // lane group g -- four consecutive threads write one 64-byte run (hi, and
 // lo 1 KiB on).  Pass 1 finds each token's largest |x| (x read once from
-// HBM), pass 2 reads the same bytes again (now from L2) and writes the
-// operands.  The work-groups cover every token slot of the last tile (slots
-// past M are zero).
+// HBM), pass 2 writes the operands from the values kept in registers (those
+// of K beyond 8192 are read again, from L2).  The work-groups cover every
+// token slot of the last tile (slots past M are zero).
 __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ x, int M, int K,
                                                       int* __restrict__ ex,
                                                       _Float16* __restrict__ xop,
@@ -59,13 +59,30 @@ __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ 
         const int gq = p >> 2, g = gq & 1, kq = gq >> 1;
         return xr + 32 * (kq >> 1) + 16 * g + 8 * (kq & 1);
     };
+    // the first CP pieces of a thread stay in registers for the second pass
+    // (all of them up to K = 8192); the rest are read again, from L2
+    constexpr int CP = 4;
+    float4 ca[CP], cb[CP];
     float mx = 0.0f;
-    for (int p = tid; p < P; p += 1024) {
+    auto amax = [](float4 a, float4 b) {
+        return fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                     fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    };
+#pragma unroll
+    for (int it = 0; it < CP; ++it) {
+        const int p = tid + 1024 * it;
+        ca[it] = cb[it] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (p < P) {
+            const float* s = src(p);
+            ca[it] = *reinterpret_cast<const float4*>(s);
+            cb[it] = *reinterpret_cast<const float4*>(s + 4);
+            mx = fmaxf(mx, amax(ca[it], cb[it]));
+        }
+    }
+    for (int p = tid + 1024 * CP; p < P; p += 1024) {
         const float* s = src(p);
-        const float4 a = *reinterpret_cast<const float4*>(s);
-        const float4 b = *reinterpret_cast<const float4*>(s + 4);
-        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                             fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+        mx = fmaxf(mx, amax(*reinterpret_cast<const float4*>(s),
+                            *reinterpret_cast<const float4*>(s + 4)));
     }
 #pragma unroll
     for (int o = 4; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
@@ -81,14 +98,11 @@ __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ 
     __syncthreads();
     const int e = es[t];
     const int T = m >> 5, lm = m & 31;
-    for (int p = tid; p < P; p += 1024) {  // P is a multiple of 64: whole waves
+    auto piece = [&](int p, float4 a, float4 b) {
         const int gq = p >> 2, g = gq & 1, kq = gq >> 1;
         h8 hi = {}, lo = {};
         float w[8] = {};
         if (live) {
-            const float* s = src(p);
-            const float4 a = *reinterpret_cast<const float4*>(s);
-            const float4 b = *reinterpret_cast<const float4*>(s + 4);
             const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int j = 0; j < 8; ++j) w[j] = __builtin_amdgcn_ldexpf(v[j], -e);
@@ -110,6 +124,16 @@ __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ 
             t8 += __shfl_xor(t8, 8, 64);
             if ((p & 12) == 0) xsum[((size_t)T * (K / 32) + (kq >> 1)) * 32 + lm] = t8;
         }
+    };
+    // P is a multiple of 64: whole waves take part in each piece's shuffles
+#pragma unroll
+    for (int it = 0; it < CP; ++it) {
+        const int p = tid + 1024 * it;
+        if (p < P) piece(p, ca[it], cb[it]);
+    }
+    for (int p = tid + 1024 * CP; p < P; p += 1024) {
+        const float* s = src(p);
+        piece(p, *reinterpret_cast<const float4*>(s), *reinterpret_cast<const float4*>(s + 4));
     }
 }
 
