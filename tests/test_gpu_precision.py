@@ -84,7 +84,7 @@ def test_small_batch_paths(dtype, M, kind):
 
 
 @pytest.mark.parametrize("kind", ["spike", "mixed"])
-@pytest.mark.parametrize("dtype", [F.Q8_0, F.Q4_0])
+@pytest.mark.parametrize("dtype", [F.Q8_0, F.Q4_0, F.Q4_1, F.Q4_K])
 def test_prefill_path(dtype, kind):
     N, K, M = 1024, 4096, 64
     w = synth.make_weights(dtype, N, K, seed=95)
