@@ -1,13 +1,15 @@
-// fq_mmqp.hip -- prefill (M > 32 tokens) for the 32-weight block formats
-// Q8_0 and Q4_0 on v_mfma_f32_32x32x16_f16.
+// fq_mmqp.hip -- prefill (M > 32 tokens) for Q8_0, Q4_0, Q4_1 and Q4_K on
+// v_mfma_f32_32x32x16_f16.
 //
 //   D[token][n] = X[token][k] . W[n][k]^T on the fp16 matrix cores, with the
 // tokens as x 2^-e(token) in fp16 hi + lo and the weights' integer codes
-// exact in fp16; one FMA per output and block folds in the block scale
-// (mmqp_kernel below).
+// exact in fp16; one FMA per output and 32-element block folds in the block
+// scale, and the formats with a per-block minimum (Q4_1, Q4_K) add it as an
+// fp32 outer product (mmqp_kernel below).
 //
 // Token prep is one launch (xprep4_kernel): the per-token exponent, then the
-// hi/lo operands in the A-operand layout.
+// hi/lo operands in the A-operand layout (and the per-token block sums for
+// the minimum term).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -37,8 +39,7 @@ constexpr int NW = 8;                // waves per work-group
 // (m % 32) + 32 g holds elements 32 (kq / 2) + 16 g + 8 (kq % 2) +
 // slot_elem(j), j = 0..7, the hi block then the lo block 512 halves on.
 //
-// One launch: work-group j owns tokens 4 j .. 4 j + 3 (all of
-// K).  Piece p = ((2 kq + g) 4 + t): token t's eight elements of quarter kq,
+// One launch: work-group j owns tokens 4 j .. 4 j + 3 (all of K).  Piece p = ((2 kq + g) 4 + t): token t's eight elements of quarter kq,
 // lane group g -- four consecutive threads write one 64-byte run (hi, and
 // lo 1 KiB on).  Pass 1 finds each token's largest |x| (x read once from
 // HBM), pass 2 writes the operands from the values kept in registers (those
@@ -349,8 +350,8 @@ struct Tile {
     static constexpr int LDS = NBUF * (XBUF + WBUF);
 };
 
-// A work-group owns 128 tokens x 256 rows and a K range (split-K when the
-// tiles alone leave CUs idle; reduce_kernel adds the slabs in split order).
+// A work-group owns 128 tokens x 256 rows and a K range (split-K when that
+// shortens the busiest CU's work; the reduce adds the slabs in split order).
 // Eight waves, each 64 tokens x 64 rows (2 x 2 tiles of 32 x 32).
 //
 // Per 32-element block b:
@@ -358,6 +359,8 @@ struct Tile {
 //   B (16 k x 32 rows):   the block's integer codes, exact in fp16,
 //   D_b = A_hi B + A_lo B  (two MFMAs per 16 k, one fp32 result per block),
 //   acc += d_b(n) D_b      (one FMA per output and block),
+//   acc -= S_b(token) m_b(n) (Q4_1, Q4_K: v_mfma_f32_32x32x2_f32 over a
+//                          step's two blocks, S_b the token's scaled sum),
 // y = 2^e(token) acc at the end.  Weights are the B operand so that a lane's
 // 16 results all belong to one row n: the block scale d_b(n) is one value
 // per lane.  x_hi + x_lo carry 22 significant bits.
