@@ -491,7 +491,7 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
 
     if (fq::mmqp_supported((int)dtype) && M > 32 && K > 0 && K % 256 == 0 &&
         (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
-        // prefill, Q8_0 / Q4_0 / Q4_1 / Q4_K rows that are whole 16-byte chunks (K
+        // prefill, Q8_0 / Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q4_K rows that are whole 16-byte chunks (K
         // a multiple of 256, 16-byte aligned weights): per-token operands, then
         // one work-group per CU and tile on v_mfma_f32_32x32x16_f16 (K-split
         // while the tiles leave CUs idle)
@@ -512,7 +512,8 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         a.w = static_cast<const uint8_t*>(w);
         a.xop = buf;
         a.ex = reinterpret_cast<const int*>(buf + al(xop_b));
-        a.xsum = dtype == FQ_DTYPE_Q4_K || dtype == FQ_DTYPE_Q4_1 ? reinterpret_cast<const float*>(buf + al(xop_b) + al(ex_b))
+        a.xsum = dtype == FQ_DTYPE_Q4_K || dtype == FQ_DTYPE_Q4_1 || dtype == FQ_DTYPE_Q5_1
+                     ? reinterpret_cast<const float*>(buf + al(xop_b) + al(ex_b))
                                : nullptr;
         a.part = splits > 1 ? reinterpret_cast<float*>(buf + al(xop_b) + al(ex_b) + al(sum_b))
                             : nullptr;

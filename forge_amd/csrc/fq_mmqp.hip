@@ -207,6 +207,33 @@ struct PB<Q4_1> {
     }
 };
 
+// Q5_0 block (22 B): d @0, qh @2 (bit j: the fifth bit of element j),
+// qs[16] @6 (element j < 16: low nibble of byte j, j + 16: high nibble),
+// value - 16.  Q5_1 block (24 B): d @0, m @2, qh @4, qs[16] @8, unsigned,
+// w = d q + m.  codes() hands ops() the lane group's 16 five-bit codes.
+template <>
+struct PB<Q5_0> {
+    static constexpr int BB = 22, SB = 2 * BB;
+    static constexpr int GS = 0, QOFF = 6, HOFF = 2;
+    static constexpr bool MIN = false;
+    template <int B>
+    __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
+        b0 = perm8(q[0], q[1], (_Float16)1040.0f);
+        b1 = perm8(q[2], q[3], (_Float16)1040.0f);
+    }
+};
+template <>
+struct PB<Q5_1> {
+    static constexpr int BB = 24, SB = 2 * BB;
+    static constexpr int GS = 0, QOFF = 8, HOFF = 4;
+    static constexpr bool MIN = true;
+    template <int B>
+    __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
+        b0 = perm8(q[0], q[1], (_Float16)1024.0f);
+        b1 = perm8(q[2], q[3], (_Float16)1024.0f);
+    }
+};
+
 // Q4_K super-block (144 B, matmul.cpp:340-377): d @0, dmin @2, scales[12]
 // @4 (6-bit scale and min per 32-element sub-block), qs[128] @16.  A step
 // (64 elements) is sub-block pair p = s mod 4 of super-block s / 4: the
@@ -238,6 +265,12 @@ struct Chunks {
     // multiple of 4 and rows 16-byte aligned)
     static constexpr int o4(int u) { return u * PB<F>::SB & 15; }
     __device__ static size_t off(int s, int) { return (size_t)s * PB<F>::SB & ~(size_t)15; }
+};
+template <>
+struct Chunks<Q5_1> {  // a step (48 bytes) starts on a chunk
+    static constexpr int CH = 3;
+    static constexpr int o4(int) { return 0; }
+    __device__ static size_t off(int s, int) { return (size_t)s * 48; }
 };
 template <>
 struct Chunks<Q4_1> {  // a step (40 bytes) starts 0 or 8 bytes into a chunk
@@ -290,6 +323,16 @@ __device__ __forceinline__ void codes(const uint8_t* row, int g, uint32_t (&q)[4
         q[1] = v[1];
         q[2] = v[2];
         q[3] = v[3];
+    } else if constexpr (F == Q5_0 || F == Q5_1) {
+        uint32_t n[4];
+        codes16<F, O4, B>(row, g, n);  // the 16 qs bytes
+        const uint32_t qh = lds4_a2(row + O4 + PB<F>::BB * B + PB<F>::HOFF) >> (16 * g);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            // fifth bits of elements 16 g + 4 k .. + 3 to bit 4 of each byte
+            const uint32_t hb = ((((qh >> (4 * k)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+            q[k] = ((n[k] >> (4 * g)) & 0x0F0F0F0Fu) | hb;
+        }
     } else {
         codes16<F, O4, B>(row, g, q);
     }
@@ -303,7 +346,7 @@ __device__ __forceinline__ void scales(const uint8_t* row, float& db, float& mn)
         Fmt<Q4_K>::scale_min(uint4{h[0], h[1], h[2], h[3]}, O4 / 4, sa, ma, sb, mb);
         db = f16_hw(h[0] & 0xFFFFu) * (float)(B ? sb : sa);
         mn = f16_hw(h[0] >> 16) * (float)(B ? mb : ma);
-    } else if constexpr (F == Q4_1) {
+    } else if constexpr (F == Q4_1 || F == Q5_1) {
         const uint32_t dm = lds4_a2(row + O4 + PB<F>::BB * B);
         db = f16_hw(dm & 0xFFFFu);
         mn = -f16_hw(dm >> 16);  // w = d q + m: the term is -(-m) S
@@ -406,6 +449,10 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
     // sub-block sums (min term): tile T, block wave & 1, lanes 0..7
     const float* ssrc = TL::MIN ? a.xsum + ((size_t)T * (a.K / 32) + (wave & 1)) * 32 + 4 * lane
                                 : nullptr;
+    // Q5_0: a 44-byte step that starts 4 bytes into its first chunk ends 16
+    // bytes before the last of its four: on the matrix's last row that chunk
+    // lies past the end (its bytes are never read)
+    const uint8_t* wend = a.w + (size_t)a.N * a.row_bytes - 16;
     const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds);
     auto issue = [&](int s) {
@@ -421,9 +468,11 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
         const uint32_t wl = lds_base + NBUF * TL::XBUF + buf * TL::WBUF + wave * 1024;
 #pragma unroll
         for (int q = 0; q < TL::WI_HI; ++q)
-            if (q < nwi)
-                dma16(wsrc[q] + Chunks<F>::off(s, TL::PLANES ? (NW * q + wave) >> 2 : 0),
-                      wl + NW * 1024 * q);
+            if (q < nwi) {
+                const uint8_t* src =
+                    wsrc[q] + Chunks<F>::off(s, TL::PLANES ? (NW * q + wave) >> 2 : 0);
+                dma16(F == Q5_0 && src > wend ? wend : src, wl + NW * 1024 * q);
+            }
     };
     // this wave's copies of step s are complete (those of step s + 1 may
     // still be in flight)
@@ -590,7 +639,8 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
 }  // namespace
 
 bool mmqp_supported(int dtype) {
-    return dtype == Q8_0 || dtype == Q4_0 || dtype == Q4_1 || dtype == Q4_K;
+    return dtype == Q8_0 || dtype == Q4_0 || dtype == Q4_1 || dtype == Q5_0 || dtype == Q5_1 ||
+           dtype == Q4_K;
 }
 int mmqp_tile_rows() { return BNT; }
 int mmqp_tile_tokens() { return BMT; }
@@ -614,6 +664,10 @@ hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st) 
         hipLaunchKernelGGL(mmqp_kernel<Q4_0>, grid, dim3(64 * NW), 0, st, a, sps);
     else if (dtype == Q4_1)
         hipLaunchKernelGGL(mmqp_kernel<Q4_1>, grid, dim3(64 * NW), 0, st, a, sps);
+    else if (dtype == Q5_0)
+        hipLaunchKernelGGL(mmqp_kernel<Q5_0>, grid, dim3(64 * NW), 0, st, a, sps);
+    else if (dtype == Q5_1)
+        hipLaunchKernelGGL(mmqp_kernel<Q5_1>, grid, dim3(64 * NW), 0, st, a, sps);
     else if (dtype == Q4_K)
         hipLaunchKernelGGL(mmqp_kernel<Q4_K>, grid, dim3(64 * NW), 0, st, a, sps);
     else

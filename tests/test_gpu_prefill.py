@@ -22,7 +22,7 @@ from test_gpu_parity import dev_weight, run
 
 pytestmark = pytest.mark.gpu
 
-PREFILL = [F.Q8_0, F.Q4_0, F.Q4_1, F.Q4_K]
+PREFILL = [F.Q8_0, F.Q4_0, F.Q4_1, F.Q4_K, F.Q5_0, F.Q5_1]
 
 
 def check(dtype, w, x, N, K, what, bias=None):
