@@ -578,7 +578,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     long pcap = 4096;
     int nl = 1;
     const void* fn =
-        gguf ? fq::gemvg_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl)
+        gguf ? fq::gemvg_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl, NV)
              : fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl,
                                    mode);
     if (gguf) {

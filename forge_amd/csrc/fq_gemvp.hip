@@ -270,53 +270,29 @@ struct Pieces {
 
 // Work distribution.  Work-group g owns the contiguous rows [lo, hi) =
 // [N g / G, N (g+1) / G).  Its work is the sequence of (K-slice, row) steps
-// in slice-major order, f = s * rows + r (a K-slice is 64 lane units), cut
-// into items of CR consecutive steps.  Waves claim items in order from an LDS
-// counter, so a wave that the SIMD arbiter serves less often simply takes
-// fewer items, and rows with many slices (long K, few rows) still spread over
-// every wave.  A wave reloads its activation limbs only when its slice
+// in slice-major order, f = s * rows + r (a K-slice is 64 lane units).  Waves
+// claim steps one at a time from an LDS counter, each claim made one step
+// before the wave needs it, so a wave that the SIMD arbiter serves less often
+// simply takes fewer steps and the work-group's waves finish within one step
+// of each other.  A wave reloads its activation limbs only when its slice
 // changes.  The row sum of step f goes to the LDS buffer part[f]; at the end
 // the work-group adds the slices of each row in slice order (so the result
-// does not depend on which wave took which item) and writes y coalesced.
-// The pipelined loop issues no global stores and no global atomics.
-constexpr int CR = 3;          // steps per item; an item spans >= D steps
+// does not depend on which wave took which step) and writes y coalesced.  The
+// pipelined loop issues no global stores and no global atomics.
 constexpr int YBUF = 4096;     // row x slice partial sums a work-group buffers in LDS
-
-struct It {
-    int f0, n, k, s, r;  // item [f0, f0 + n), step k of it = (slice s, row r)
-};
 
 struct Claims {
     int* ctr;
     int total, rows;
+    float inv_rows;
 };
 
-// Uniform claim of the next item from the work-group's LDS counter.
-__device__ __forceinline__ It item(const Claims& cl, int i) {
-    const int f0 = i * CR;
-    if (f0 >= cl.total) return It{0, 0, 0, 0, 0};
-    const int s = f0 / cl.rows;
-    return It{f0, min(CR, cl.total - f0), 0, s, f0 - s * cl.rows};
-}
-
-__device__ __forceinline__ It claim(const Claims& cl, int lane) {
+// Uniform claim of the next step (-1: none left).
+__device__ __forceinline__ int claim(const Claims& cl, int lane) {
     int i = 0;
     if (lane == 0) i = atomicAdd(cl.ctr, 1);
-    return item(cl, __builtin_amdgcn_readfirstlane(i));
-}
-
-// The item the load side has claimed beyond the compute side's item (n = 0:
-// none).  Every item but the last spans CR >= D steps, so the load side, D
-// steps ahead, is at most one item ahead and one slot suffices.  Uniform
-// scalars only: an indexed queue would live in scratch memory, whose loads
-// share the in-order vector memory counter with the weight loads and drain
-// them.
-__device__ __forceinline__ void next_step(It& t, int rows) {
-    ++t.k;
-    if (++t.r == rows) {
-        t.r = 0;
-        ++t.s;
-    }
+    i = __builtin_amdgcn_readfirstlane(i);
+    return i < cl.total ? i : -1;
 }
 
 // Row sources.  ONE: row v of a.w.  PAIR: two matrices of the same shape
@@ -348,26 +324,26 @@ struct RegSel<F, 0> {
 
 // First byte of step t's K-slice in a GGUF row.
 template <int F, int NL, int MODE>
-__device__ __forceinline__ const uint8_t* gslice(const GemvArgs& a, const It& t, int lo) {
-    return row_ptr<MODE>(a, min(lo + t.r, a.N - 1)) + (size_t)t.s * slice_bytes<F, NL>();
+__device__ __forceinline__ const uint8_t* gslice(const GemvArgs& a, int sl, int r, int lo) {
+    return row_ptr<MODE>(a, min(lo + r, a.N - 1)) + (size_t)sl * slice_bytes<F, NL>();
 }
 
 template <int F, int NL, int MODE, int GP>
 __device__ __forceinline__ void pload(typename RegSel<F, GP>::T (&f)[NL], const GemvArgs& a,
-                                      const It& t, int lo, int lane) {
+                                      int sl, int row, int lo, int lane) {
     if constexpr (GP == 0) {
-        const uint8_t* r = row_ptr<MODE>(a, min(lo + t.r, a.N - 1));
-        const int v0 = t.s * 64 * NL;
+        const uint8_t* r = row_ptr<MODE>(a, min(lo + row, a.N - 1));
+        const int v0 = sl * 64 * NL;
 #pragma unroll
         for (int c = 0; c < NL; ++c)
             f[c] = Pk<F>::load(r, min(v0 + lane + 64 * c, a.U - 1), a.U);
     } else {
         // pointer arithmetic (not integer casts) keeps the global address
         // space, so these stay global_load (vmcnt only)
-        const uint8_t* g0 = gslice<F, NL, MODE>(a, t, lo);
+        const uint8_t* g0 = gslice<F, NL, MODE>(a, sl, row, lo);
         const int shift = (int)(reinterpret_cast<uintptr_t>(g0) & 15);
         const uint8_t* a0 = g0 - shift;
-        const int units = min(64 * NL, a.U - 64 * NL * t.s);
+        const int units = min(64 * NL, a.U - 64 * NL * sl);
         const int n16 = (shift + units / Gk<F>::UPB * Gk<F>::BB + 15) >> 4;
 #pragma unroll
         for (int i = 0; i < GP; ++i) f[0].v[i] = ldg128<true>(a0 + 16 * min(lane + 64 * i, n16 - 1));
@@ -384,29 +360,35 @@ __device__ __forceinline__ void load_slice_limbs(Limbs (&L)[NL][Pk<F>::NREC], co
             read_limbs(L[c][r], lds, min(s * 64 * NL + lane + 64 * c, U - 1) * Pk<F>::NREC + r);
 }
 
-__device__ __forceinline__ void advance_load(It& ld, It& q, const Claims& cl, int lane) {
-    if (ld.n == 0) return;
-    next_step(ld, cl.rows);
-    if (ld.k == ld.n) {
-        ld = claim(cl, lane);
-        if (ld.n > 0) q = ld;
-    }
+// The slot's step (-1: none) as (slice, row).  f < rows * slices <= YBUF:
+// (f + 0.5) / rows in fp32 lies at least 0.5 / rows from an integer and is
+// off by at most 2^-22 (f / rows) <= 2^-10 / rows, so its floor is exact.
+struct Step {
+    int f, s, r;
+};
+__device__ __forceinline__ Step step_of(int f, int rows, float inv_rows) {
+    const int s = f >= 0 ? (int)(((float)f + 0.5f) * inv_rows) : 0;
+    return Step{f, s, f >= 0 ? f - s * rows : 0};
 }
 
-// One step of the compute side (slice cp.s of row lo + cp.r), then the loads
-// of the load side's step into the same registers.
+// One slot of the pipeline: the compute side of the step whose loads the
+// slot holds, then the loads of the wave's next claimed step into the same
+// registers (past the last step they load row lo again, so the number of
+// loads in flight never varies).
 // GGUF (GP > 0): the step's pieces go to the wave's LDS buffer wbuf first,
 // the next loads are issued into the freed registers, then each lane reads
 // its unit from the buffer.  A wave's LDS accesses execute in order, so no
 // barrier separates the writes from the reads.
-template <int F, int NL, int D, bool BIAS, int MODE, int GP>
-__device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], It& cp, It& ld, It& q,
+template <int F, int NL, int MODE, int GP>
+__device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& st, int& nxt,
                                       const Claims& cl, const GemvArgs& a,
                                       Limbs (&L)[NL][Pk<F>::NREC], const uint8_t* lds,
-                                      uint8_t* wbuf, float* part, int lo, int lane, int& cur_s,
-                                      float& res) {
+                                      uint8_t* wbuf, float* part, int lo, int lane, int& cur_s) {
     __builtin_amdgcn_sched_barrier(0);
-    if (cp.s != cur_s) {  // wave-uniform
+    const Step cp = st;
+    st = step_of(nxt, cl.rows, cl.inv_rows);
+    if (nxt >= 0) nxt = claim(cl, lane);  // wave-uniform
+    if (cp.f >= 0 && cp.s != cur_s) {  // wave-uniform
         load_slice_limbs<F, NL>(L, lds, cp.s, a.U, lane);
         cur_s = cp.s;
     }
@@ -419,17 +401,17 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], It& cp
             const float t = Pk<F>::dot(f[c], min(v, a.U - 1), L[c]);
             acc += v < a.U ? t : 0.0f;
         }
-        pload<F, NL, MODE, GP>(f, a, ld, lo, lane);
+        pload<F, NL, MODE, GP>(f, a, st.s, st.r, lo, lane);
     } else {
 #pragma unroll
         for (int i = 0; i < GP; ++i) reinterpret_cast<uint4*>(wbuf)[lane + 64 * i] = f[0].v[i];
         const int shift =
-            (int)(reinterpret_cast<uintptr_t>(gslice<F, NL, MODE>(a, cp, lo)) & 15);
+            (int)(reinterpret_cast<uintptr_t>(gslice<F, NL, MODE>(a, cp.s, cp.r, lo)) & 15);
         typename Pk<F>::Raw raw[NL];
 #pragma unroll
         for (int c = 0; c < NL; ++c)
             raw[c] = Gk<F>::read(wbuf + shift, min(v0 + lane + 64 * c, a.U - 1) - v0);
-        pload<F, NL, MODE, GP>(f, a, ld, lo, lane);
+        pload<F, NL, MODE, GP>(f, a, st.s, st.r, lo, lane);
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
             const int v = v0 + lane + 64 * c;
@@ -437,21 +419,8 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], It& cp
             acc += v < a.U ? t : 0.0f;
         }
     }
-    const float s = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum(acc)), 63));
-    // advance the compute side; a finished item goes to the LDS partial buffer
-    if (cp.n > 0) {  // wave-uniform; past the last item the step only keeps the loads in step
-        res = lane == cp.k ? res + s : res;
-        next_step(cp, cl.rows);
-        if (cp.k == cp.n) {
-            if (lane < cp.n) part[cp.f0 + lane] = res;
-            res = 0.0f;
-            cp = q;
-            q.n = 0;
-        }
-    }
-    // after the compute side has taken the pending item, so the slot is free
-    advance_load(ld, q, cl, lane);
+    const float sum = wave_sum(acc);
+    if (cp.f >= 0 && lane == 63) part[cp.f] = sum;
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -464,7 +433,6 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], It& cp
 template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE, int GP = 0>
 __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     constexpr bool DUAL = MODE == PAIR;
-    static_assert(D <= CR, "an item must span at least D steps");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int ctr;
     constexpr int W = WG / 64;
@@ -486,44 +454,42 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     const int hi = DUAL ? 2 * (int)((int64_t)(a.N / 2) * (g + 1) / G)
                         : (int)((int64_t)a.N * (g + 1) / G);
     const int rows = hi - lo;
-    const Claims cl{&ctr, rows * ns, rows};
+    const Claims cl{&ctr, rows * ns, rows, 1.0f / (float)max(rows, 1)};
 
-    // limb records first, so the activation loads never queue behind the
-    // weight stream; then the first D steps of weight loads
-    // item w is wave w's first (the counter hands out the rest); its first
-    // step's weight loads go out between the activation loads and the limb
-    // build, so HBM is busy during the staging without delaying the
-    // activations (the remaining first loads follow the barrier: issued all
-    // at once they would queue ahead of other work-groups' activation loads)
-    if (threadIdx.x == 0) ctr = W;
-    It q{0, 0, 0, 0, 0};
-    It ld = item(cl, __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6)), cp = ld;
+    // Wave w's first D steps are w, W + w, ..., and its first claim is
+    // D W + w; the counter hands out the rest from (D + 1) W.  The activation
+    // loads go first, so they never queue behind the weight stream; the first
+    // step's weight loads go out between them and the limb build, so HBM is
+    // busy during the staging without delaying the activations (the remaining
+    // first loads follow the barrier: issued all at once they would queue
+    // ahead of other work-groups' activation loads).
+    if (threadIdx.x == 0) ctr = (D + 1) * W;
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    Step st[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) st[j] = step_of(j * W + w < cl.total ? j * W + w : -1, rows, cl.inv_rows);
+    int nxt = D * W + w < cl.total ? D * W + w : -1;
     typename RegSel<F, GP>::T f[D][NL];
     {
         XStage<P, WG> xs;
         stage_load<P, WG>(xs, a.x, a.Uc, 0);
-        pload<F, NL, MODE, GP>(f[0], a, ld, lo, lane);
+        pload<F, NL, MODE, GP>(f[0], a, st[0].s, st[0].r, lo, lane);
         stage_build<P, WG, false>(lds, xs, a.x, a.Uc, 0);
     }
     lds_barrier();  // the weight loads stay in flight
-    advance_load(ld, q, cl, lane);
 #pragma unroll
-    for (int j = 1; j < D; ++j) {
-        pload<F, NL, MODE, GP>(f[j], a, ld, lo, lane);
-        advance_load(ld, q, cl, lane);
-    }
+    for (int j = 1; j < D; ++j) pload<F, NL, MODE, GP>(f[j], a, st[j].s, st[j].r, lo, lane);
     Limbs L[NL][P::NREC];
-    float res = 0.0f;
     int cur_s = -1;
-    // every iteration runs all D steps, each issuing its loads, so the number
+    // every iteration runs all D slots, each issuing its loads, so the number
     // of loads in flight at the loop head is always the same and the compiler
-    // waits for exactly one step's loads (a skipped step would make it drain
-    // the whole queue)
-    while (cp.n > 0) {
+    // waits for exactly one slot's loads (a skipped load would make it drain
+    // the whole queue); steps are claimed in order, so once slot 0 holds no
+    // step neither does any later slot
+    while (st[0].f >= 0) {
 #pragma unroll
         for (int j = 0; j < D; ++j)
-            pstep<F, NL, D, BIAS, MODE, GP>(f[j], cp, ld, q, cl, a, L, lds, wbuf, part, lo, lane,
-                                            cur_s, res);
+            pstep<F, NL, MODE, GP>(f[j], st[j], nxt, cl, a, L, lds, wbuf, part, lo, lane, cur_s);
     }
     __syncthreads();
     if constexpr (DUAL) {
@@ -548,7 +514,13 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
 }
 
 constexpr int WGP = 1024;
-constexpr int DP = 3;
+// Steps of weight loads a wave keeps in flight.  One, with 16 waves per CU,
+// measured fastest at every packed shape (cfg2 gate 10.3 us against 10.7 with
+// two and 12.3 with three).  GGUF rows of matrices of 64k rows and more
+// (lm_head) keep three: 81.4 us against 86.3 with one.
+constexpr int DP = 1;
+constexpr int DPG_DEEP = 3;
+constexpr int DEEP_ROWS = 65536;
 
 // Two lane units per lane hold both units' activation limbs in registers:
 // more than the 128 VGPRs of a 1024-thread work-group, so they run 512.
@@ -571,7 +543,9 @@ const void* pfn2(bool bias) {
 template <int F>
 const void* pfn(int units, bool bias, int* nl) {
     *nl = lane_units<F>(units);
-    return *nl == 2 ? pfn2<F, 2>(bias) : pfn2<F, 1>(bias);
+    if constexpr (F == Q4_0 || F == Q4_1)
+        if (*nl == 2) return pfn2<F, 2>(bias);
+    return pfn2<F, 1>(bias);
 }
 
 template <int F>
@@ -594,35 +568,38 @@ constexpr int gwg() {
     return GP >= 4 ? 512 : WGP;
 }
 
+template <int F, int NL, int GP, int D>
+const void* gfn3(bool bias) {
+    constexpr int WG = nl_wg<NL, gwg<GP>()>();
+    return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, D, true, WG, ONE, GP>)
+                : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, D, false, WG, ONE, GP>);
+}
+
 template <int F, int NL, int GP>
-const void* gfn2(bool bias) {
+const void* gfn2(bool bias, bool deep) {
     if constexpr (GP > max_pieces<F>() * NL) {
         return nullptr;
     } else {
-        constexpr int WG = nl_wg<NL, gwg<GP>()>();
-        return bias
-                   ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, depth<NL>(), true, WG, ONE, GP>)
-                   : reinterpret_cast<const void*>(
-                         &gemvp_kernel<F, NL, depth<NL>(), false, WG, ONE, GP>);
+        return deep ? gfn3<F, NL, GP, DPG_DEEP>(bias) : gfn3<F, NL, GP, depth<NL>()>(bias);
     }
 }
 
 template <int F>
-const void* gfn(int units, bool bias, int* gp, int* nl) {
+const void* gfn(int units, bool bias, bool deep, int* gp, int* nl) {
     *nl = lane_units<F>(units);
     *gp = slice_pieces<F>(units < 64 * *nl ? units : 64 * *nl);
-    if (*nl == 2) {
-        switch (*gp) {
-            case 2: return gfn2<F, 2, 2>(bias);
-            case 3: return gfn2<F, 2, 3>(bias);
+    if constexpr (F == Q4_0 || F == Q4_1) {
+        if (*nl == 2) switch (*gp) {
+            case 2: return gfn2<F, 2, 2>(bias, deep);
+            case 3: return gfn2<F, 2, 3>(bias, deep);
             default: return nullptr;
         }
     }
     switch (*gp) {
-        case 1: return gfn2<F, 1, 1>(bias);
-        case 2: return gfn2<F, 1, 2>(bias);
-        case 3: return gfn2<F, 1, 3>(bias);
-        case 4: return gfn2<F, 1, 4>(bias);
+        case 1: return gfn2<F, 1, 1>(bias, deep);
+        case 2: return gfn2<F, 1, 2>(bias, deep);
+        case 3: return gfn2<F, 1, 3>(bias, deep);
+        case 4: return gfn2<F, 1, 4>(bias, deep);
         default: return nullptr;
     }
 }
@@ -664,16 +641,17 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
 // buffer).  *lds_fixed: the records and the wave buffers; the host adds the
 // partial-sum buffer after them.
 const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
-                            int* wg, int* nl) {
+                            int* wg, int* nl, int rows) {
     int gp = 0;
+    const bool deep = rows >= DEEP_ROWS;
     const void* fn = nullptr;
     *nl = 1;
     switch (dtype) {
-        case Q4_0: fn = gfn<Q4_0>(units, bias, &gp, nl); break;
-        case Q4_1: fn = gfn<Q4_1>(units, bias, &gp, nl); break;
-        case Q8_0: fn = gfn<Q8_0>(units, bias, &gp, nl); break;
-        case Q4_K: fn = gfn<Q4_K>(units, bias, &gp, nl); break;
-        case Q6_K: fn = gfn<Q6_K>(units, bias, &gp, nl); break;
+        case Q4_0: fn = gfn<Q4_0>(units, bias, deep, &gp, nl); break;
+        case Q4_1: fn = gfn<Q4_1>(units, bias, deep, &gp, nl); break;
+        case Q8_0: fn = gfn<Q8_0>(units, bias, deep, &gp, nl); break;
+        case Q4_K: fn = gfn<Q4_K>(units, bias, deep, &gp, nl); break;
+        case Q6_K: fn = gfn<Q6_K>(units, bias, deep, &gp, nl); break;
     }
     *wg = *nl == 2 ? nl_wg<2, WGP>() : gp >= 4 ? gwg<4>() : WGP;
     *lds_fixed = (size_t)records * RECB + (size_t)(*wg / 64) * gp * 1024;
