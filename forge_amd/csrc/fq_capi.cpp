@@ -285,7 +285,8 @@ int noalloc_workspace(int dev, uint8_t** out) {
 
 int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
                 const void* w3_packed, int n1, int n2, int mode, const float* bias,
-                int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf);
+                int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf, int M = 1,
+                bool bias_full = false);
 
 int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias, int bias_mode,
                int64_t bias_len, float* y, int M, int K, int N, hipStream_t st, uint8_t* fixed,
@@ -319,6 +320,16 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         const int rc = packed_gemv(dtype, x, w, nullptr, nullptr, 0, 0, 0,
                                    bias_mode ? bias : nullptr, bias_mode == 2 ? N : bias_len, y,
                                    K, N, st, true);
+        if (rc != FQ_ERR_SHAPE) return rc;
+    }
+
+    if (M == 2 && K > 0 && packable(dtype) &&
+        (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
+        // two tokens: the same kernel dots each weight unit it reads with both
+        // tokens' limbs (FQ_ERR_SHAPE: both tokens' records do not fit LDS)
+        const int rc = packed_gemv(dtype, x, w, nullptr, nullptr, 0, 0, 0,
+                                   bias_mode ? bias : nullptr, bias_mode == 2 ? N : bias_len, y,
+                                   K, N, st, true, 2, bias_mode == 2);
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
@@ -546,13 +557,15 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
 // caller has validated the arguments as run_matmul does).
 int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
                 const void* w3_packed, int n1, int n2, int mode, const float* bias,
-                int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf) {
+                int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf, int M,
+                bool bias_full) {
     Geometry g;
     if (!geometry(dtype, g) || !packable(dtype)) return FQ_ERR_DTYPE;
     if (N < 0 || K < 0 || K % (gguf ? g.be : 256) != 0) return FQ_ERR_SHAPE;
     if (N == 0) return FQ_OK;
     if (!x || !w_packed || !y) return FQ_ERR_NULL;
     if (gguf && mode != 0) return FQ_ERR_SHAPE;
+    if (M != 1 && !(gguf && M == 2)) return FQ_ERR_SHAPE;
     const uintptr_t amask = gguf ? 1 : 15;
     if ((reinterpret_cast<uintptr_t>(w_packed) & amask) != 0) return FQ_ERR_ALIGN;
     for (const void* p : {w2_packed, w3_packed})
@@ -578,12 +591,14 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     long pcap = 4096;
     int nl = 1;
     const void* fn =
-        gguf ? fq::gemvg_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl, NV)
+        gguf ? fq::gemvg_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl, NV,
+                                   M)
              : fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl,
                                    mode);
     if (gguf) {
-        if (lds + 64 * 4 > lds_cap) return FQ_ERR_SHAPE;
-        pcap = std::min<long>(4096, (long)(lds_cap - lds) / 4);
+        // M tokens' partial sums per row and K-slice
+        if (lds + 64 * 4 * M > lds_cap) return FQ_ERR_SHAPE;
+        pcap = std::min<long>(4096, (long)(lds_cap - lds) / (4 * M));
     }
     if (!fn || lds > lds_cap) return FQ_ERR_SHAPE;
     int per_cu = 0;
@@ -601,7 +616,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     auto max_rows = [&](long g) { return dual ? 2 * ((N + g - 1) / g) : (NV + g - 1) / g; };
     G = std::max<long>(G, ((long)NV * ns + pcap - 1) / pcap);
     while (max_rows(G) * ns > pcap) ++G;
-    if (gguf) lds += 4 * (size_t)(max_rows(G) * ns);
+    if (gguf) lds += 4 * (size_t)M * (max_rows(G) * ns);
     fq::GemvArgs a{};
     a.x = x;
     a.w = static_cast<const uint8_t*>(w_packed);
@@ -612,8 +627,8 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     a.y = y;
     a.bias = bias;
     a.bias_len = bias ? bias_len : 0;
-    a.bias_mode = bias ? 1 : 0;
-    a.M = 1;
+    a.bias_mode = bias ? (bias_full ? 2 : 1) : 0;
+    a.M = M;
     a.K = K;
     a.N = NV;
     a.U = units;

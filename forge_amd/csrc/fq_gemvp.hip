@@ -379,27 +379,34 @@ __device__ __forceinline__ Step step_of(int f, int rows, float inv_rows) {
 // the next loads are issued into the freed registers, then each lane reads
 // its unit from the buffer.  A wave's LDS accesses execute in order, so no
 // barrier separates the writes from the reads.
-template <int F, int NL, int MODE, int GP>
+template <int F, int NL, int MODE, int GP, int NT>
 __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& st, int& nxt,
                                       const Claims& cl, const GemvArgs& a,
-                                      Limbs (&L)[NL][Pk<F>::NREC], const uint8_t* lds,
+                                      Limbs (&L)[NT][NL][Pk<F>::NREC], const uint8_t* lds,
                                       uint8_t* wbuf, float* part, int lo, int lane, int& cur_s) {
     __builtin_amdgcn_sched_barrier(0);
     const Step cp = st;
     st = step_of(nxt, cl.rows, cl.inv_rows);
     if (nxt >= 0) nxt = claim(cl, lane);  // wave-uniform
     if (cp.f >= 0 && cp.s != cur_s) {  // wave-uniform
-        load_slice_limbs<F, NL>(L, lds, cp.s, a.U, lane);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            load_slice_limbs<F, NL>(L[t], lds + (size_t)t * a.Uc * RECB, cp.s, a.U, lane);
         cur_s = cp.s;
     }
     const int v0 = cp.s * 64 * NL;
-    float acc = 0.0f;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
     if constexpr (GP == 0) {
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
             const int v = v0 + lane + 64 * c;
-            const float t = Pk<F>::dot(f[c], min(v, a.U - 1), L[c]);
-            acc += v < a.U ? t : 0.0f;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float d = Pk<F>::dot(f[c], min(v, a.U - 1), L[t][c]);
+                acc[t] += v < a.U ? d : 0.0f;
+            }
         }
         pload<F, NL, MODE, GP>(f, a, st.s, st.r, lo, lane);
     } else {
@@ -415,12 +422,18 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& 
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
             const int v = v0 + lane + 64 * c;
-            const float t = Pk<F>::dot(raw[c], min(v, a.U - 1), L[c]);
-            acc += v < a.U ? t : 0.0f;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float d = Pk<F>::dot(raw[c], min(v, a.U - 1), L[t][c]);
+                acc[t] += v < a.U ? d : 0.0f;
+            }
         }
     }
-    const float sum = wave_sum(acc);
-    if (cp.f >= 0 && lane == 63) part[cp.f] = sum;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float sum = wave_sum(acc[t]);
+        if (cp.f >= 0 && lane == 63) part[t * cl.total + cp.f] = sum;
+    }
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -429,9 +442,13 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& 
 // even.  MODE CAT: y is the concatenation of the three GEMVs (fused QKV).
 // GP > 0: GGUF rows, GP pieces per lane per K-slice; the dynamic LDS holds
 // the limb records, then one GP KiB buffer per wave, then the partial sums
-// (sized by the host).
-template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE, int GP = 0>
+// (sized by the host).  NT tokens (MODE ONE, GGUF rows): every weight unit
+// read and decoded once is dotted with each token's limbs; token t's records
+// follow token t - 1's, and y, the partial sums and a full bias
+// (a.bias_mode 2) are token-major.
+template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE, int GP = 0, int NT = 1>
 __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
+    static_assert(NT == 1 || (MODE == ONE && GP > 0), "several tokens: GGUF rows, MODE ONE");
     constexpr bool DUAL = MODE == PAIR;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int ctr;
@@ -442,8 +459,8 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
         __shared__ float part_s[YBUF];
         part = part_s;
     } else {
-        wbuf = lds + (size_t)a.Uc * RECB + (threadIdx.x >> 6) * (GP * 1024);
-        part = reinterpret_cast<float*>(lds + (size_t)a.Uc * RECB + W * GP * 1024);
+        wbuf = lds + (size_t)NT * a.Uc * RECB + (threadIdx.x >> 6) * (GP * 1024);
+        part = reinterpret_cast<float*>(lds + (size_t)NT * a.Uc * RECB + W * GP * 1024);
     }
     using P = Pk<F>;
     const int lane = threadIdx.x & 63;
@@ -472,14 +489,14 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     typename RegSel<F, GP>::T f[D][NL];
     {
         XStage<P, WG> xs;
-        stage_load<P, WG>(xs, a.x, a.Uc, 0);
+        stage_load<P, WG>(xs, a.x, NT * a.Uc, 0, NT > 1 ? a.Uc : 0, a.K);
         pload<F, NL, MODE, GP>(f[0], a, st[0].s, st[0].r, lo, lane);
-        stage_build<P, WG, false>(lds, xs, a.x, a.Uc, 0);
+        stage_build<P, WG, false>(lds, xs, a.x, NT * a.Uc, 0, NT > 1 ? a.Uc : 0, a.K);
     }
     lds_barrier();  // the weight loads stay in flight
 #pragma unroll
     for (int j = 1; j < D; ++j) pload<F, NL, MODE, GP>(f[j], a, st[j].s, st[j].r, lo, lane);
-    Limbs L[NL][P::NREC];
+    Limbs L[NT][NL][P::NREC];
     int cur_s = -1;
     // every iteration runs all D slots, each issuing its loads, so the number
     // of loads in flight at the loop head is always the same and the compiler
@@ -489,7 +506,7 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     while (st[0].f >= 0) {
 #pragma unroll
         for (int j = 0; j < D; ++j)
-            pstep<F, NL, MODE, GP>(f[j], st[j], nxt, cl, a, L, lds, wbuf, part, lo, lane, cur_s);
+            pstep<F, NL, MODE, GP, NT>(f[j], st[j], nxt, cl, a, L, lds, wbuf, part, lo, lane, cur_s);
     }
     __syncthreads();
     if constexpr (DUAL) {
@@ -504,11 +521,15 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     } else {
         // the bias is added to the finished row sum, as apply_bias adds it to
         // the finished product (matmul.cpp:1005-1049)
-        for (int r = threadIdx.x; r < rows; r += WG) {
-            float v = part[r];
-            for (int s = 1; s < ns; ++s) v += part[s * rows + r];
-            if constexpr (BIAS) v += lo + r < a.bias_len ? a.bias[lo + r] : 0.0f;
-            a.y[lo + r] = v;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float* bias = a.bias + (a.bias_mode == 2 ? (size_t)t * a.N : 0);
+            for (int r = threadIdx.x; r < rows; r += WG) {
+                float v = part[t * cl.total + r];
+                for (int s = 1; s < ns; ++s) v += part[t * cl.total + s * rows + r];
+                if constexpr (BIAS) v += lo + r < a.bias_len ? bias[lo + r] : 0.0f;
+                a.y[(size_t)t * a.N + lo + r] = v;
+            }
         }
     }
 }
@@ -604,6 +625,46 @@ const void* gfn(int units, bool bias, bool deep, int* gp, int* nl) {
     }
 }
 
+// Two tokens: both tokens' limbs stay in registers, more than the 128 VGPRs
+// of a 1024-thread work-group.  One lane unit per lane fits 168 (768
+// threads: cfg3 M = 2 12.5-13.5 us against 13.3 at 512, GGUF lm_head 101
+// against 107); two lane units need ~235, so 512 threads.
+template <int NL>
+constexpr int wg_t2() {
+    return NL == 2 ? 512 : 768;
+}
+
+template <int F, int NL, int GP>
+const void* gfn_t2(bool bias) {
+    if constexpr (GP > max_pieces<F>() * NL) {
+        return nullptr;
+    } else {
+        constexpr int WG = wg_t2<NL>();
+        return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, true, WG, ONE, GP, 2>)
+                    : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, false, WG, ONE, GP, 2>);
+    }
+}
+
+template <int F>
+const void* gfn2t(int units, bool bias, int* gp, int* nl) {
+    *nl = lane_units<F>(units);
+    *gp = slice_pieces<F>(units < 64 * *nl ? units : 64 * *nl);
+    if constexpr (F == Q4_0 || F == Q4_1) {
+        if (*nl == 2) switch (*gp) {
+            case 2: return gfn_t2<F, 2, 2>(bias);
+            case 3: return gfn_t2<F, 2, 3>(bias);
+            default: return nullptr;
+        }
+    }
+    switch (*gp) {
+        case 1: return gfn_t2<F, 1, 1>(bias);
+        case 2: return gfn_t2<F, 1, 2>(bias);
+        case 3: return gfn_t2<F, 1, 3>(bias);
+        case 4: return gfn_t2<F, 1, 4>(bias);
+        default: return nullptr;
+    }
+}
+
 }  // namespace
 
 // Lane units per row and activation records for a packed GEMV of length K.
@@ -641,11 +702,24 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
 // buffer).  *lds_fixed: the records and the wave buffers; the host adds the
 // partial-sum buffer after them.
 const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
-                            int* wg, int* nl, int rows) {
+                            int* wg, int* nl, int rows, int tokens) {
     int gp = 0;
     const bool deep = rows >= DEEP_ROWS;
     const void* fn = nullptr;
     *nl = 1;
+    if (tokens == 2) {
+        switch (dtype) {
+            case Q4_0: fn = gfn2t<Q4_0>(units, bias, &gp, nl); break;
+            case Q4_1: fn = gfn2t<Q4_1>(units, bias, &gp, nl); break;
+            case Q8_0: fn = gfn2t<Q8_0>(units, bias, &gp, nl); break;
+            case Q4_K: fn = gfn2t<Q4_K>(units, bias, &gp, nl); break;
+            case Q6_K: fn = gfn2t<Q6_K>(units, bias, &gp, nl); break;
+        }
+        *wg = *nl == 2 ? wg_t2<2>() : wg_t2<1>();
+        *lds_fixed = 2 * (size_t)records * RECB + (size_t)(*wg / 64) * gp * 1024;
+        return fn;
+    }
+    if (tokens != 1) return nullptr;
     switch (dtype) {
         case Q4_0: fn = gfn<Q4_0>(units, bias, deep, &gp, nl); break;
         case Q4_1: fn = gfn<Q4_1>(units, bias, deep, &gp, nl); break;

@@ -120,6 +120,31 @@ def test_small_batch_config3(M):
     check_shape(F.Q4_K, 14336, 4096, M, seed=3000 + M, what=f"cfg3 M={M}")
 
 
+@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K])
+@pytest.mark.parametrize("N,K", [(4099, 4096), (2053, 7168), (700, 18944)])
+def test_two_tokens_batch1_kernel(dtype, N, K):
+    # M = 2 on weights of 8 MB and more (every Q6_K): the batch-1 kernel dots
+    # each weight unit with both tokens' limbs.  Each token's arithmetic and
+    # summation order are the batch-1 kernel's, so token t's row equals the
+    # M = 1 result bit for bit; the oracle pins one token.  Every bias form
+    # is added after the sum.  At K = 18944 two tokens' records need more LDS
+    # than there is and the call falls back to the other kernels, which the
+    # oracle check still covers.
+    w = synth.make_weights(dtype, N, K, seed=50 + dtype)
+    x = synth.make_x(2, K, 51 + N)
+    y = run(dtype, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(dtype, w, N, K))))
+    assert_close(y, oracle.matmul_f64(dtype, x, w, N, K), x, np.array([deq_max]),
+                 f"{F.fmt(dtype).name} M=2 {N}x{K}")
+    if K != 18944:
+        for t in range(2):
+            np.testing.assert_array_equal(y[t], run(dtype, w, x[t:t + 1], N, K)[0])
+    b1 = torch.linspace(-1, 1, N)
+    np.testing.assert_allclose(run(dtype, w, x, N, K, bias=b1), y + b1.numpy(), rtol=1e-6, atol=1e-6)
+    b2 = torch.randn(2, N)
+    np.testing.assert_allclose(run(dtype, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q6_K, F.Q5_0, F.Q5_1, F.Q3_K,
                                    F.Q5_K, F.IQ4_NL])
 @pytest.mark.parametrize("M", [2, 5, 16])
