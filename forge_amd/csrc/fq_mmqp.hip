@@ -15,6 +15,7 @@
 
 #include <type_traits>
 
+#include "fq_dma.h"
 #include "fq_formats.h"
 #include "fq_kernels.h"
 #include "fq_limbs.h"
@@ -354,22 +355,6 @@ __device__ __forceinline__ void scales(const uint8_t* row, float& db, float& mn)
         db = f16_hw(*reinterpret_cast<const uint16_t*>(row + O4 + PB<F>::BB * B));
         mn = 0.0f;
     }
-}
-
-// Global memory straight into LDS: 16 bytes per lane, to lds + 16 lane (lds
-// is wave-uniform, in M0).  Issued as inline assembly on
-// purpose: the compiler cannot tell which LDS bytes the builtin's copy
-// writes, so it waits for every outstanding load (vmcnt(0)) before the next
-// LDS read, which would serialise each step's loads with the step's compute.
-// The kernel counts the copies itself (wait_step) before the barrier that
-// publishes them.
-__device__ __forceinline__ void dma16(const uint8_t* g, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(lds) : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
 template <int F>
