@@ -56,12 +56,14 @@ def traffic(fetch_csv, write_csv, copy_mib, kernel, grid, lds):
     f, w = counter_groups(fetch_csv), counter_groups(write_csv)
     kib = copy_mib * 1024.0
 
-    def copy_val(groups):
-        vals = [v for (n, _, _), v in groups.items() if "copyBuffer" in n or "copy" in n.lower()]
-        best = max(vals)  # the calibration copy is by far the largest copy
-        return best
+    def copy_val(path):
+        # the calibration copy is by far the largest single copy dispatch
+        # (copies of other sizes share its kernel name and grid, so group
+        # means would mix them in)
+        return max(float(r["Counter_Value"]) for r in csv.DictReader(open(path))
+                   if "copy" in r["Kernel_Name"].lower())
 
-    cf, cw = copy_val(f) / kib, copy_val(w) / kib
+    cf, cw = copy_val(fetch_csv) / kib, copy_val(write_csv) / kib
     key = [k for k in f if k[0].startswith(kernel) and k[1] == grid and k[2] == lds]
     if len(key) != 1:
         raise SystemExit(f"kernel shape not found uniquely: {key}")
