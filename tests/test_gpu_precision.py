@@ -74,9 +74,10 @@ def test_batch1_gguf_and_packed(dtype, N, K, kind):
 @pytest.mark.parametrize("M", [2, 3, 5, 8, 16])
 @pytest.mark.parametrize("dtype", [F.Q4_K, F.Q6_K, F.Q8_0])
 def test_small_batch_paths(dtype, M, kind):
-    # cfg3-like rows (Q4_K M = 3..8 runs on the int8 matrix cores, M = 2 on the
-    # two-token row step, M = 16 on the fp16 MFMA path)
-    N, K = 2048, 4096
+    # cfg3-like rows (Q4_K M = 3 runs on the int8 matrix cores, M = 5..16 on
+    # the one-pass fp16 MFMA kernel; M = 2 on the batch-1 kernel with two
+    # tokens, which takes weights of 8 MB and more, so 4096 rows there)
+    N, K = (4096 if M == 2 else 2048), 4096
     w = synth.make_weights(dtype, N, K, seed=80 + M)
     x = outlier_x(M, K, 90 + M, kind)
     y = ops.matmul_transB(torch.from_numpy(x).cuda(), dev_weight(dtype, w, N, K))
@@ -84,7 +85,7 @@ def test_small_batch_paths(dtype, M, kind):
 
 
 @pytest.mark.parametrize("kind", ["spike", "mixed"])
-@pytest.mark.parametrize("dtype", [F.Q8_0, F.Q4_0, F.Q4_1, F.Q4_K])
+@pytest.mark.parametrize("dtype", [F.Q8_0, F.Q4_0, F.Q4_1, F.Q4_K, F.Q5_0, F.Q5_1])
 def test_prefill_path(dtype, kind):
     N, K, M = 1024, 4096, 64
     w = synth.make_weights(dtype, N, K, seed=95)
