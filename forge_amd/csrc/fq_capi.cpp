@@ -597,8 +597,9 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
                                    mode);
     if (gguf) {
         // M tokens' partial sums per row and K-slice
-        if (lds + 64 * 4 * M > lds_cap) return FQ_ERR_SHAPE;
-        pcap = std::min<long>(4096, (long)(lds_cap - lds) / (4 * M));
+        // (256 bytes left for the kernel's static LDS: its step counter)
+        if (lds + 64 * 4 * M + 256 > lds_cap) return FQ_ERR_SHAPE;
+        pcap = std::min<long>(4096, (long)(lds_cap - lds - 256) / (4 * M));
     }
     if (!fn || lds > lds_cap) return FQ_ERR_SHAPE;
     int per_cu = 0;

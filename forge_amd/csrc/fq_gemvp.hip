@@ -582,16 +582,18 @@ constexpr int max_pieces() {
     return slice_pieces<F>(64);
 }
 
-// Four pieces per lane need more than the 128 VGPRs of a 1024-thread
-// work-group (D steps of pieces plus the unit and the limbs): 512 threads.
-template <int GP>
+// Four pieces per lane with three steps in flight need more than the 128
+// VGPRs of a 1024-thread work-group: 512 threads.  With one step in flight
+// they fit (92 VGPRs): cfg2 down on GGUF bytes 16.6-19.3 us against
+// 18.9-21.1 at 512 threads.
+template <int GP, int D>
 constexpr int gwg() {
-    return GP >= 4 ? 512 : WGP;
+    return GP >= 4 && D > 1 ? 512 : WGP;
 }
 
 template <int F, int NL, int GP, int D>
 const void* gfn3(bool bias) {
-    constexpr int WG = nl_wg<NL, gwg<GP>()>();
+    constexpr int WG = nl_wg<NL, gwg<GP, D>()>();
     return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, D, true, WG, ONE, GP>)
                 : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, D, false, WG, ONE, GP>);
 }
@@ -727,7 +729,7 @@ const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t
         case Q4_K: fn = gfn<Q4_K>(units, bias, deep, &gp, nl); break;
         case Q6_K: fn = gfn<Q6_K>(units, bias, deep, &gp, nl); break;
     }
-    *wg = *nl == 2 ? nl_wg<2, WGP>() : gp >= 4 ? gwg<4>() : WGP;
+    *wg = *nl == 2 ? nl_wg<2, WGP>() : gp >= 4 && deep ? gwg<4, DPG_DEEP>() : WGP;
     *lds_fixed = (size_t)records * RECB + (size_t)(*wg / 64) * gp * 1024;
     return fn;
 }
