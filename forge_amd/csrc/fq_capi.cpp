@@ -323,13 +323,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
-    if (M == 2 && K > 0 && packable(dtype) &&
+    if (M >= 2 && M <= 4 && K > 0 && packable(dtype) &&
         (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
-        // two tokens: the same kernel dots each weight unit it reads with both
-        // tokens' limbs (FQ_ERR_SHAPE: both tokens' records do not fit LDS)
+        // two to four tokens: the same kernel dots each weight unit it reads
+        // with every token's limbs (FQ_ERR_SHAPE: the tokens' records do not
+        // fit LDS)
         const int rc = packed_gemv(dtype, x, w, nullptr, nullptr, 0, 0, 0,
                                    bias_mode ? bias : nullptr, bias_mode == 2 ? N : bias_len, y,
-                                   K, N, st, true, 2, bias_mode == 2);
+                                   K, N, st, true, M, bias_mode == 2);
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
@@ -565,7 +566,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     if (N == 0) return FQ_OK;
     if (!x || !w_packed || !y) return FQ_ERR_NULL;
     if (gguf && mode != 0) return FQ_ERR_SHAPE;
-    if (M != 1 && !(gguf && M == 2)) return FQ_ERR_SHAPE;
+    if (M != 1 && !(gguf && M >= 2 && M <= 4)) return FQ_ERR_SHAPE;
     const uintptr_t amask = gguf ? 1 : 15;
     if ((reinterpret_cast<uintptr_t>(w_packed) & amask) != 0) return FQ_ERR_ALIGN;
     for (const void* p : {w2_packed, w3_packed})

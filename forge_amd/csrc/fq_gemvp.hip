@@ -627,44 +627,67 @@ const void* gfn(int units, bool bias, bool deep, int* gp, int* nl) {
     }
 }
 
-// Two tokens: both tokens' limbs stay in registers, more than the 128 VGPRs
-// of a 1024-thread work-group.  One lane unit per lane fits 168 (768
-// threads: cfg3 M = 2 12.5-13.5 us against 13.3 at 512, GGUF lm_head 101
-// against 107); two lane units need ~235, so 512 threads.
-template <int NL>
-constexpr int wg_t2() {
-    return NL == 2 ? 512 : 768;
+// Two to four tokens: every token's limbs stay in registers, more than the
+// 128 VGPRs of a 1024-thread work-group.  Two tokens with one lane unit per
+// lane fit 168 (768 threads: cfg3 M = 2 12.5-13.5 us against 13.3 at 512,
+// GGUF lm_head 101 against 107); two lane units, or three and four tokens,
+// need up to 256, so 512 threads (three and four tokens: one lane unit).
+// Three tokens against the other kernels: cfg3 Q4_K 16.3 against 20.7 us,
+// Q6_K lm_head 128 against 227, Q8_0 14336 x 4096 19.3 against 22.7; four
+// tokens (Q4_0, Q4_1, Q8_0): Q8_0 22.7 against 26.4.
+template <int NL, int NT>
+constexpr int wg_t() {
+    return NL == 2 || NT > 2 ? 512 : 768;
 }
 
-template <int F, int NL, int GP>
-const void* gfn_t2(bool bias) {
+template <int F, int NL, int GP, int NT>
+const void* gfn_t(bool bias) {
     if constexpr (GP > max_pieces<F>() * NL) {
         return nullptr;
     } else {
-        constexpr int WG = wg_t2<NL>();
-        return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, true, WG, ONE, GP, 2>)
-                    : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, false, WG, ONE, GP, 2>);
+        constexpr int WG = wg_t<NL, NT>();
+        return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, true, WG, ONE, GP, NT>)
+                    : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, false, WG, ONE, GP, NT>);
+    }
+}
+
+template <int F, int NT>
+const void* gfnt(int units, bool bias, int* gp, int* nl) {
+    *nl = lane_units<F>(units);
+    *gp = slice_pieces<F>(units < 64 * *nl ? units : 64 * *nl);
+    if constexpr (F == Q4_0 || F == Q4_1) {
+        if (*nl == 2) {
+            if constexpr (NT == 2) {
+                switch (*gp) {
+                    case 2: return gfn_t<F, 2, 2, NT>(bias);
+                    case 3: return gfn_t<F, 2, 3, NT>(bias);
+                }
+            }
+            return nullptr;
+        }
+    }
+    switch (*gp) {
+        case 1: return gfn_t<F, 1, 1, NT>(bias);
+        case 2: return gfn_t<F, 1, 2, NT>(bias);
+        case 3: return gfn_t<F, 1, 3, NT>(bias);
+        case 4: return gfn_t<F, 1, 4, NT>(bias);
+        default: return nullptr;
     }
 }
 
 template <int F>
-const void* gfn2t(int units, bool bias, int* gp, int* nl) {
-    *nl = lane_units<F>(units);
-    *gp = slice_pieces<F>(units < 64 * *nl ? units : 64 * *nl);
-    if constexpr (F == Q4_0 || F == Q4_1) {
-        if (*nl == 2) switch (*gp) {
-            case 2: return gfn_t2<F, 2, 2>(bias);
-            case 3: return gfn_t2<F, 2, 3>(bias);
-            default: return nullptr;
-        }
+const void* gfn_tokens(int tokens, int units, bool bias, int* gp, int* nl) {
+    switch (tokens) {
+        case 2: return gfnt<F, 2>(units, bias, gp, nl);
+        case 3: return gfnt<F, 3>(units, bias, gp, nl);
+        case 4:
+            // Q4_K and Q6_K units hold two records per token: four tokens'
+            // limbs spill (Q6_K lm_head at M = 4 271 us against 257 on the
+            // other kernels, cfg3 Q4_K 21.1 against 20.7)
+            if constexpr (F == Q4_K || F == Q6_K) return nullptr;
+            else return gfnt<F, 4>(units, bias, gp, nl);
     }
-    switch (*gp) {
-        case 1: return gfn_t2<F, 1, 1>(bias);
-        case 2: return gfn_t2<F, 1, 2>(bias);
-        case 3: return gfn_t2<F, 1, 3>(bias);
-        case 4: return gfn_t2<F, 1, 4>(bias);
-        default: return nullptr;
-    }
+    return nullptr;
 }
 
 }  // namespace
@@ -709,16 +732,16 @@ const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t
     const bool deep = rows >= DEEP_ROWS;
     const void* fn = nullptr;
     *nl = 1;
-    if (tokens == 2) {
+    if (tokens >= 2) {
         switch (dtype) {
-            case Q4_0: fn = gfn2t<Q4_0>(units, bias, &gp, nl); break;
-            case Q4_1: fn = gfn2t<Q4_1>(units, bias, &gp, nl); break;
-            case Q8_0: fn = gfn2t<Q8_0>(units, bias, &gp, nl); break;
-            case Q4_K: fn = gfn2t<Q4_K>(units, bias, &gp, nl); break;
-            case Q6_K: fn = gfn2t<Q6_K>(units, bias, &gp, nl); break;
+            case Q4_0: fn = gfn_tokens<Q4_0>(tokens, units, bias, &gp, nl); break;
+            case Q4_1: fn = gfn_tokens<Q4_1>(tokens, units, bias, &gp, nl); break;
+            case Q8_0: fn = gfn_tokens<Q8_0>(tokens, units, bias, &gp, nl); break;
+            case Q4_K: fn = gfn_tokens<Q4_K>(tokens, units, bias, &gp, nl); break;
+            case Q6_K: fn = gfn_tokens<Q6_K>(tokens, units, bias, &gp, nl); break;
         }
-        *wg = *nl == 2 ? wg_t2<2>() : wg_t2<1>();
-        *lds_fixed = 2 * (size_t)records * RECB + (size_t)(*wg / 64) * gp * 1024;
+        *wg = *nl == 2 ? 512 : tokens > 2 ? 512 : 768;
+        *lds_fixed = (size_t)tokens * records * RECB + (size_t)(*wg / 64) * gp * 1024;
         return fn;
     }
     if (tokens != 1) return nullptr;

@@ -120,28 +120,36 @@ def test_small_batch_config3(M):
     check_shape(F.Q4_K, 14336, 4096, M, seed=3000 + M, what=f"cfg3 M={M}")
 
 
+@pytest.mark.parametrize("M", [2, 3, 4])
 @pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K])
-@pytest.mark.parametrize("N,K", [(4099, 4096), (2053, 7168), (700, 18944)])
-def test_two_tokens_batch1_kernel(dtype, N, K):
-    # M = 2 on weights of 8 MB and more (every Q6_K): the batch-1 kernel dots
-    # each weight unit with both tokens' limbs.  Each token's arithmetic and
-    # summation order are the batch-1 kernel's, so token t's row equals the
-    # M = 1 result bit for bit; the oracle pins one token.  Every bias form
-    # is added after the sum.  At K = 18944 two tokens' records need more LDS
-    # than there is and the call falls back to the other kernels, which the
-    # oracle check still covers.
+@pytest.mark.parametrize("N,K", [(4099, 4096), (2113, 7168), (700, 18944)])
+def test_few_tokens_batch1_kernel(dtype, N, K, M):
+    # M = 2 .. 4 on weights of 8 MB and more (every Q6_K; below that M = 1 and
+    # M > 1 take other kernels): the batch-1 kernel
+    # dots each weight unit with every token's limbs (Q4_K and Q6_K: up to
+    # three tokens; Q4_0 and Q4_1 rows of two lane units: two).  Each token's
+    # arithmetic and summation order are the batch-1 kernel's, so where the
+    # call takes that kernel token t's row equals the M = 1 result bit for
+    # bit; the oracle pins every case.  Every bias form is added after the
+    # sum.  At K = 18944 the tokens' records need more LDS than there is and
+    # the call falls back to the other kernels.
     w = synth.make_weights(dtype, N, K, seed=50 + dtype)
-    x = synth.make_x(2, K, 51 + N)
+    x = synth.make_x(M, K, 51 + N + M)
     y = run(dtype, w, x, N, K)
     deq_max = float(np.max(np.abs(oracle.dequant(dtype, w, N, K))))
     assert_close(y, oracle.matmul_f64(dtype, x, w, N, K), x, np.array([deq_max]),
-                 f"{F.fmt(dtype).name} M=2 {N}x{K}")
-    if K != 18944:
-        for t in range(2):
+                 f"{F.fmt(dtype).name} M={M} {N}x{K}")
+    fm = F.fmt(dtype)
+    units = K // 32  # 32-element units
+    big = dtype == F.Q6_K or N * (K // fm.block_elems) * fm.block_bytes >= 8 << 20
+    batch1 = (big and K != 18944 and not (M == 4 and dtype in (F.Q4_K, F.Q6_K))
+              and not (M > 2 and dtype in (F.Q4_0, F.Q4_1) and units > 64))
+    if batch1:
+        for t in range(M):
             np.testing.assert_array_equal(y[t], run(dtype, w, x[t:t + 1], N, K)[0])
     b1 = torch.linspace(-1, 1, N)
     np.testing.assert_allclose(run(dtype, w, x, N, K, bias=b1), y + b1.numpy(), rtol=1e-6, atol=1e-6)
-    b2 = torch.randn(2, N)
+    b2 = torch.randn(M, N)
     np.testing.assert_allclose(run(dtype, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6, atol=1e-6)
 
 
