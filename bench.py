@@ -614,7 +614,7 @@ def all_configs(cpu=False):
     for n, dt, N, K in [("gate", Q4_K, 18944, 3584), ("down", Q6_K, 3584, 18944),
                         ("lm_head", Q6_K, 152064, 3584)]:
         add(f"cfg2-{n}", dt, N, K, 1, packed_too=True)
-    for M in (1, 2, 4, 8, 16):
+    for M in (1, 2, 3, 4, 8, 16):
         add("cfg3", Q4_K, 14336, 4096, M, packed_too=M == 1)
     for dt in (Q8_0, Q4_0):
         for N in (4096, 14336):
