@@ -502,9 +502,11 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     }
 
     if (fq::mmqp_supported((int)dtype) && M > 32 && K > 0 && K % 256 == 0 &&
-        (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+        (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+        (int64_t)N * ((K / g.be) * g.bb) < ((int64_t)1 << 32)) {
         // prefill, Q8_0 / Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q4_K rows that are whole 16-byte chunks (K
-        // a multiple of 256, 16-byte aligned weights): per-token operands, then
+        // a multiple of 256, 16-byte aligned weights, under 4 GiB of them:
+        // the copies take 32-bit offsets): per-token operands, then
         // one work-group per CU and tile on v_mfma_f32_32x32x16_f16 (K-split
         // while the tiles leave CUs idle)
         const MmqpPlan pl = plan_mmqp(M, K, N, di.cus);

@@ -18,6 +18,17 @@ __device__ __forceinline__ void dma16(const uint8_t* g, uint32_t lds) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(lds) : "memory");
 }
 
+// The same copy from base + off: base wave-uniform (a scalar register pair),
+// off a 32-bit per-lane byte offset, so a loop that moves base keeps the
+// per-lane part in one register and its address arithmetic on the scalar
+// unit.
+__device__ __forceinline__ void dma16s(uint32_t off, const uint8_t* base, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(off), "s"(base), "{m0}"(lds)
+                 : "memory");
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vm() {

@@ -418,10 +418,12 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
     // wave) + lane of the row-major [row][CH] step tile (rows clamped to a
     // real row)
     const int T = min(m0 / 32 + (wave >> 1), Tn - 1);
-    const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(a.xop) +
-                          ((size_t)T * KQ * XT) * 2 + (wave & 1) * 4096 + 16 * lane;
+    // wave-uniform bases (scalar registers) and per-lane 32-bit offsets (the
+    // host keeps the weights under 4 GiB)
+    const uint8_t* const xbase =
+        reinterpret_cast<const uint8_t*>(a.xop) + ((size_t)T * KQ * XT) * 2 + (wave & 1) * 4096;
     const int nwi = wave < TL::W_HI ? TL::WI_HI : TL::WI_LO;  // wave-uniform
-    const uint8_t* wsrc[TL::WI_HI];
+    uint32_t woff[TL::WI_HI];
 #pragma unroll
     for (int q = 0; q < TL::WI_HI; ++q) {
         const int L = min(64 * (NW * q + wave) + lane, TL::WCH - 1);
@@ -429,34 +431,36 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
         // instruction k = NW q + wave is plane k / 4, wave-uniform
         const int r = TL::PLANES ? L % BNT : L / TL::CH;
         const int p = TL::PLANES ? L / BNT : L - r * TL::CH;
-        wsrc[q] = a.w + (size_t)min(n0 + r, a.N - 1) * a.row_bytes + 16 * p;
+        woff[q] = (uint32_t)min(n0 + r, a.N - 1) * (uint32_t)a.row_bytes + 16 * p;
     }
     // sub-block sums (min term): tile T, block wave & 1, lanes 0..7
-    const float* ssrc = TL::MIN ? a.xsum + ((size_t)T * (a.K / 32) + (wave & 1)) * 32 + 4 * lane
-                                : nullptr;
+    const float* const sbase =
+        TL::MIN ? a.xsum + ((size_t)T * (a.K / 32) + (wave & 1)) * 32 : nullptr;
     // Q5_0: a 44-byte step that starts 4 bytes into its first chunk ends 16
     // bytes before the last of its four: on the matrix's last row that chunk
     // lies past the end (its bytes are never read)
-    const uint8_t* wend = a.w + (size_t)a.N * a.row_bytes - 16;
+    const uint32_t wend = (uint32_t)a.N * (uint32_t)a.row_bytes - 16;
     const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds);
     auto issue = [&](int s) {
         const int buf = s % NBUF;
         const uint32_t xl = lds_base + buf * TL::XBUF + wave * 4096;
-        const uint8_t* xg = xsrc + (size_t)s * 4 * XT * 2;
+        const uint8_t* xg = xbase + (size_t)s * 4 * XT * 2;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dma16(xg + 1024 * i, xl + 1024 * i);
+        for (int i = 0; i < 4; ++i) dma16s(16 * lane + 1024 * i, xg, xl + 1024 * i);
         if constexpr (TL::MIN) {
             const uint32_t sl = lds_base + buf * TL::XBUF + TL::XOPB + wave * 128;
-            if (lane < 8) dma16(reinterpret_cast<const uint8_t*>(ssrc + (size_t)64 * s), sl);
+            if (lane < 8)
+                dma16s(16 * lane, reinterpret_cast<const uint8_t*>(sbase + (size_t)64 * s), sl);
         }
         const uint32_t wl = lds_base + NBUF * TL::XBUF + buf * TL::WBUF + wave * 1024;
 #pragma unroll
         for (int q = 0; q < TL::WI_HI; ++q)
             if (q < nwi) {
-                const uint8_t* src =
-                    wsrc[q] + Chunks<F>::off(s, TL::PLANES ? (NW * q + wave) >> 2 : 0);
-                dma16(F == Q5_0 && src > wend ? wend : src, wl + NW * 1024 * q);
+                const uint32_t so =
+                    (uint32_t)Chunks<F>::off(s, TL::PLANES ? (NW * q + wave) >> 2 : 0);
+                const uint32_t vo = F == Q5_0 ? min(woff[q], wend - so) : woff[q];
+                dma16s(vo, a.w + so, wl + NW * 1024 * q);
             }
     };
     // this wave's copies of step s are complete (those of step s + 1 may
