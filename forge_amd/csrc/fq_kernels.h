@@ -19,7 +19,8 @@ struct GemvArgs {
     int bias_mode;        // 0 none, 1 row vector over n, 2 full [M][N]
     int M, K, N;
     int U;                // 32-weight units per row (K / 32)
-    int Uc;               // units per K-split
+    int Uc;               // kernel-specific count: batch-1 activation records per
+                          // token (gemvp), units or steps per chunk (the others)
     int row_bytes;
 };
 
