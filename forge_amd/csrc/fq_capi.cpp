@@ -556,8 +556,8 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
 // gate/up): y[n] = silu(x . w[n]) * (x . w2[n]), run as one GEMV over 2 N
 // interleaved rows.  mode 2 (fused QKV): y = [x . w | x . w2 | x . w3] with
 // n1 and n2 rows in w and w2 and N rows in all.
-// gguf: the same kernel over the unmodified GGUF rows (mode 0 only; the
-// caller has validated the arguments as run_matmul does).
+// gguf: the same kernel over the unmodified GGUF rows (the caller has
+// validated the arguments as run_matmul does).
 int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
                 const void* w3_packed, int n1, int n2, int mode, const float* bias,
                 int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf, int M,
@@ -567,8 +567,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     if (N < 0 || K < 0 || K % (gguf ? g.be : 256) != 0) return FQ_ERR_SHAPE;
     if (N == 0) return FQ_OK;
     if (!x || !w_packed || !y) return FQ_ERR_NULL;
-    if (gguf && mode != 0) return FQ_ERR_SHAPE;
-    if (M != 1 && !(gguf && M >= 2 && M <= 4)) return FQ_ERR_SHAPE;
+    if (M != 1 && !(gguf && mode == 0 && M >= 2 && M <= 4)) return FQ_ERR_SHAPE;
     const uintptr_t amask = gguf ? 1 : 15;
     if ((reinterpret_cast<uintptr_t>(w_packed) & amask) != 0) return FQ_ERR_ALIGN;
     for (const void* p : {w2_packed, w3_packed})
@@ -595,7 +594,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     int nl = 1;
     const void* fn =
         gguf ? fq::gemvg_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl, NV,
-                                   M)
+                                   M, mode)
              : fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl,
                                    mode);
     if (gguf) {
@@ -810,6 +809,14 @@ int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk,
     const void* ws[3] = {wq, wk, wv};
     const int ns[3] = {Nq, Nk, Nv};
     if (M == 1) {  // the three outputs are contiguous slices of y
+        // one launch over the three matrices' GGUF rows when the batch-1
+        // kernel takes them (8 MB and more in all, or Q6_K)
+        if (packable(dtype) && Nq && Nk && Nv &&
+            (dtype == FQ_DTYPE_Q6_K || (int64_t)Nt * (K / g.be) * g.bb >= (8 << 20))) {
+            const int rc = packed_gemv(dtype, x, wq, wk, wv, Nq, Nk, 2, nullptr, 0, y, K, Nt, st,
+                                       true);
+            if (rc != FQ_ERR_SHAPE) return rc;
+        }
         int off = 0;
         for (int i = 0; i < 3; ++i) {
             if (ns[i] > 0) {
@@ -865,6 +872,14 @@ int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const vo
     if (M == 0 || N == 0) return FQ_OK;
     if (!x || !w_gate || !w_up || !y) return FQ_ERR_NULL;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (M == 1 && packable(dtype) &&
+        (dtype == FQ_DTYPE_Q6_K || 2 * (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
+        // one launch: gate and up rows interleaved, silu(gate) * up in the
+        // epilogue, straight from the GGUF bytes
+        const int rc = packed_gemv(dtype, x, w_gate, w_up, nullptr, 0, 0, 1, nullptr, 0, y, K, N,
+                                   st, true);
+        if (rc != FQ_ERR_SHAPE) return rc;
+    }
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e);

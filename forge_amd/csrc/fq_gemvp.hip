@@ -690,6 +690,31 @@ const void* gfn_tokens(int tokens, int units, bool bias, int* gp, int* nl) {
     return nullptr;
 }
 
+// The fused forms (MODE PAIR: gate/up; CAT: QKV) over GGUF rows: one lane
+// unit per lane, one step of loads in flight.
+template <int F, int MODE, int GP>
+const void* gfn_mode3() {
+    if constexpr (GP > max_pieces<F>()) {
+        return nullptr;
+    } else {
+        return reinterpret_cast<const void*>(
+            &gemvp_kernel<F, 1, DP, false, gwg<GP, DP>(), MODE, GP>);
+    }
+}
+
+template <int F>
+const void* gfn_mode(int mode, int units, int* gp) {
+    *gp = slice_pieces<F>(units < 64 ? units : 64);
+    const bool pair = mode == PAIR;
+    switch (*gp) {
+        case 1: return pair ? gfn_mode3<F, PAIR, 1>() : gfn_mode3<F, CAT, 1>();
+        case 2: return pair ? gfn_mode3<F, PAIR, 2>() : gfn_mode3<F, CAT, 2>();
+        case 3: return pair ? gfn_mode3<F, PAIR, 3>() : gfn_mode3<F, CAT, 3>();
+        case 4: return pair ? gfn_mode3<F, PAIR, 4>() : gfn_mode3<F, CAT, 4>();
+    }
+    return nullptr;
+}
+
 }  // namespace
 
 // Lane units per row and activation records for a packed GEMV of length K.
@@ -727,11 +752,24 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
 // buffer).  *lds_fixed: the records and the wave buffers; the host adds the
 // partial-sum buffer after them.
 const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
-                            int* wg, int* nl, int rows, int tokens) {
+                            int* wg, int* nl, int rows, int tokens, int mode) {
     int gp = 0;
     const bool deep = rows >= DEEP_ROWS;
     const void* fn = nullptr;
     *nl = 1;
+    if (mode) {
+        if (tokens != 1 || bias) return nullptr;
+        switch (dtype) {
+            case Q4_0: fn = gfn_mode<Q4_0>(mode, units, &gp); break;
+            case Q4_1: fn = gfn_mode<Q4_1>(mode, units, &gp); break;
+            case Q8_0: fn = gfn_mode<Q8_0>(mode, units, &gp); break;
+            case Q4_K: fn = gfn_mode<Q4_K>(mode, units, &gp); break;
+            case Q6_K: fn = gfn_mode<Q6_K>(mode, units, &gp); break;
+        }
+        *wg = gp >= 4 ? gwg<4, DP>() : WGP;
+        *lds_fixed = (size_t)records * RECB + (size_t)(*wg / 64) * gp * 1024;
+        return fn;
+    }
     if (tokens >= 2) {
         switch (dtype) {
             case Q4_0: fn = gfn_tokens<Q4_0>(tokens, units, bias, &gp, nl); break;

@@ -42,10 +42,11 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
                             int* nl, int mode = 0);
 // the same kernel over GGUF rows; *lds_fixed excludes the partial-sum buffer
 // (4 bytes per token, row and K-slice of a work-group, placed after it);
-// rows: the matrix's rows (the load depth depends on it); tokens: 1 or 2
-// (y, a full bias and x token-major)
+// rows: the matrix's rows (the load depth depends on it); tokens: 1 … 4
+// (y, a full bias and x token-major); mode 1 / 2: the fused gate/up and QKV
+// forms, one token, no bias
 const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
-                            int* wg, int* nl, int rows, int tokens = 1);
+                            int* wg, int* nl, int rows, int tokens = 1, int mode = 0);
 hipError_t launch_pack(int dtype, const uint8_t* src, uint8_t* dst, int N, int K, bool pack,
                        int grid, hipStream_t st);
 hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st);

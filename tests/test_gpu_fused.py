@@ -79,6 +79,49 @@ def test_fused_packed(name, dtype, N, K):
     assert torch.equal(y, y2), "fused packed GEMV is not deterministic"
 
 
+@pytest.mark.parametrize("name,dtype,N,K", [
+    ("cfg2-gate-up", F.Q4_K, 18944, 3584),
+    ("q4_0-7b-gate-up", F.Q4_0, 18944, 3584),
+    ("q6k-long-k", F.Q6_K, 700, 18944),
+    ("q8_0", F.Q8_0, 1100, 4096),
+])
+def test_fused_gguf_one_launch(name, dtype, N, K):
+    # M = 1 on GGUF bytes of 8 MB and more (every Q6_K): gate and up rows
+    # interleaved in one batch-1 launch with silu(gate) * up in its epilogue;
+    # the same gate and up as the two unfused GEMVs (same kernel arithmetic),
+    # and deterministic
+    wg, wu = make(dtype, N, K, 17)
+    x = synth.make_x(1, K, seed=18)
+    Wg, Wu = dev_weight(dtype, wg, N, K), dev_weight(dtype, wu, N, K)
+    xd = torch.from_numpy(x).cuda()
+    y = ops.ffn_up_fused(xd, Wg, Wu)
+    check(y.cpu().numpy(), dtype, x, wg, wu, N, K, name)
+    g = ops.matmul_transB(xd, Wg).double().cpu().numpy()
+    u = ops.matmul_transB(xd, Wu).double().cpu().numpy()
+    assert_close_silu_mul(y.cpu().numpy(), g, u, x, wmax(dtype, (wg[:4096], wu[:4096]), K),
+                          name + " vs unfused")
+    assert torch.equal(y, ops.ffn_up_fused(xd, Wg, Wu)), "fused GGUF GEMV is not deterministic"
+
+
+@pytest.mark.parametrize("name,dtype,K,Nq,Nk,Nv", [
+    ("qwen7b-q4_k", F.Q4_K, 3584, 3584, 512, 512),
+    ("q8_0", F.Q8_0, 4096, 2048, 512, 512),
+    ("q6_k-odd", F.Q6_K, 1024, 77, 5, 33),
+])
+def test_fused_qkv_gguf_one_launch(name, dtype, K, Nq, Nk, Nv):
+    # M = 1 on GGUF bytes of 8 MB and more in all (every Q6_K): the three
+    # matrices' rows in one batch-1 launch, y their concatenation
+    ns = (Nq, Nk, Nv)
+    ws = [synth.make_weights(dtype, n, K, 50 + i) for i, n in enumerate(ns)]
+    x = synth.make_x(1, K, seed=55)
+    xd = torch.from_numpy(x).cuda()
+    Ws = [dev_weight(dtype, w, n, K) for w, n in zip(ws, ns)]
+    y = ops.fused_qkv(xd, *Ws)
+    ref = np.concatenate([oracle.matmul_f64(dtype, x, w, n, K) for w, n in zip(ws, ns)], axis=1)
+    assert_matmul(y.cpu().numpy().reshape(1, -1), ref, x, ws, dtype, K, name)
+    assert torch.equal(y, ops.fused_qkv(xd, *Ws)), "fused QKV is not deterministic"
+
+
 def test_fused_errors():
     N, K = 64, 256
     wg, wu = make(F.Q4_0, N, K, 1)
