@@ -530,7 +530,8 @@ def measured_traffic():
 
 def time_fused(name, dtype, N, K, reps=20, pool_bytes=600 << 20):
     """Average device time of the fused gate/up (fq_ffn_up_fused_packed, one
-    launch) next to the two separate packed GEMVs, both HIP-graph replays."""
+    launch) next to the two separate packed GEMVs and to the operator path's
+    fq_ffn_up_fused on the GGUF bytes, all HIP-graph replays."""
     import torch
     from forge_amd import _lib, ops, synth
     L = _lib.lib()
@@ -540,7 +541,7 @@ def time_fused(name, dtype, N, K, reps=20, pool_bytes=600 << 20):
     for c in range(copies):
         g = ops.QWeight.from_numpy(synth.make_weights(dtype, N, K, seed=3 * c), dtype, N, K)
         u = ops.QWeight.from_numpy(synth.make_weights(dtype, N, K, seed=3 * c + 1), dtype, N, K)
-        pairs.append((ops.pack_weights(g), ops.pack_weights(u)))
+        pairs.append((ops.pack_weights(g), ops.pack_weights(u), g, u))
         del g, u
     x = torch.from_numpy(synth.make_x(1, K, 1)).cuda()
     y = torch.empty(N, device="cuda")
@@ -557,8 +558,13 @@ def time_fused(name, dtype, N, K, reps=20, pool_bytes=600 << 20):
             assert L.fq_gemv_packed(dtype, x.data_ptr(), w.data.data_ptr(), None, 0,
                                     out.data_ptr(), K, N, st) == 0
 
+    def gguf_fused(p, st):  # the operator path: fq_ffn_up_fused on the GGUF bytes
+        assert L.fq_ffn_up_fused(dtype, x.data_ptr(), p[2].data.data_ptr(), p[3].data.data_ptr(),
+                                 y.data_ptr(), 1, K, N, st) == 0
+
     out = {"config": name, "M": 1, "N": N, "K": K, "op": "ffn_up_fused (gate+up+SiLU)"}
-    for label, fn in (("fused_us", fused), ("two_gemv_us", separate)):
+    for label, fn in (("fused_us", fused), ("two_gemv_us", separate),
+                      ("gguf_fused_us", gguf_fused)):
         for p in pairs:
             fn(p, side.cuda_stream)
         torch.cuda.synchronize()
