@@ -811,10 +811,12 @@ int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk,
     if (M == 1) {  // the three outputs are contiguous slices of y
         // one launch over the three matrices' GGUF rows when the batch-1
         // kernel takes them (8 MB and more in all, or Q6_K)
-        if (packable(dtype) && Nq && Nk && Nv &&
+        if (packable(dtype) &&
             (dtype == FQ_DTYPE_Q6_K || (int64_t)Nt * (K / g.be) * g.bb >= (8 << 20))) {
-            const int rc = packed_gemv(dtype, x, wq, wk, wv, Nq, Nk, 2, nullptr, 0, y, K, Nt, st,
-                                       true);
+            // a matrix of no rows is never read: any valid pointer stands in
+            const void* any = Nq ? wq : Nk ? wk : wv;
+            const int rc = packed_gemv(dtype, x, Nq ? wq : any, Nk ? wk : any, Nv ? wv : any, Nq,
+                                       Nk, 2, nullptr, 0, y, K, Nt, st, true);
             if (rc != FQ_ERR_SHAPE) return rc;
         }
         int off = 0;

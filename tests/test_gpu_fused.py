@@ -107,18 +107,24 @@ def test_fused_gguf_one_launch(name, dtype, N, K):
     ("qwen7b-q4_k", F.Q4_K, 3584, 3584, 512, 512),
     ("q8_0", F.Q8_0, 4096, 2048, 512, 512),
     ("q6_k-odd", F.Q6_K, 1024, 77, 5, 33),
+    ("dual-q4_k", F.Q4_K, 3584, 2048, 2048, 0),  # matmul_transB_dual: two matrices
+    ("q6_k-no-q", F.Q6_K, 1024, 0, 40, 33),
 ])
 def test_fused_qkv_gguf_one_launch(name, dtype, K, Nq, Nk, Nv):
     # M = 1 on GGUF bytes of 8 MB and more in all (every Q6_K): the three
     # matrices' rows in one batch-1 launch, y their concatenation
     ns = (Nq, Nk, Nv)
-    ws = [synth.make_weights(dtype, n, K, 50 + i) for i, n in enumerate(ns)]
+    ws = [synth.make_weights(dtype, max(n, 1), K, 50 + i) for i, n in enumerate(ns)]
     x = synth.make_x(1, K, seed=55)
     xd = torch.from_numpy(x).cuda()
-    Ws = [dev_weight(dtype, w, n, K) for w, n in zip(ws, ns)]
+    Ws = [dev_weight(dtype, w, max(n, 1), K) for w, n in zip(ws, ns)]
+    for W, n in zip(Ws, ns):
+        W.N = n  # a zero-row matrix keeps a valid buffer
     y = ops.fused_qkv(xd, *Ws)
-    ref = np.concatenate([oracle.matmul_f64(dtype, x, w, n, K) for w, n in zip(ws, ns)], axis=1)
-    assert_matmul(y.cpu().numpy().reshape(1, -1), ref, x, ws, dtype, K, name)
+    ref = np.concatenate([oracle.matmul_f64(dtype, x, w, n, K) if n else np.zeros((1, 0))
+                          for w, n in zip(ws, ns)], axis=1)
+    assert_matmul(y.cpu().numpy().reshape(1, -1), ref, x, [w for w, n in zip(ws, ns) if n],
+                  dtype, K, name)
     assert torch.equal(y, ops.fused_qkv(xd, *Ws)), "fused QKV is not deterministic"
 
 
