@@ -47,6 +47,11 @@ def test_noalloc_matches_two_calls(dtype):
 def test_noalloc_every_m_path():
     for M in (1, 2, 3, 5, 33):
         _pair(F.Q4_K, M, 2048, 640, 50 + M)
+    # the batch-1 kernel with 1 .. 4 tokens (Q6_K always takes it) and the
+    # one-pass small-batch kernel on 8 MB of Q4_K
+    for M in (1, 2, 3, 4):
+        _pair(F.Q6_K, M, 2048, 3000, 70 + M, bias=M == 3)
+    _pair(F.Q4_K, 8, 4096, 4096, 80)
 
 
 def test_noalloc_prefill_and_limit():
