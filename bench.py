@@ -312,6 +312,18 @@ class StepRunner:
         events on the launch stream around the whole region."""
         import torch
         nk = len(CFG2)
+        # steps for ~WARM_SECONDS first (not counted as warm-up steps): the GPU
+        # idles while the host makes the weights, and its clocks need that
+        # long to come back up
+        t_end = time.perf_counter() + WARM_SECONDS
+        s = 0
+        while time.perf_counter() < t_end:
+            for i in range(nk):
+                self.launch(i, self.sets[s % 2][i])
+            s += 1
+            if s % 16 == 0:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
         for s in range(warmup):
             for i in range(nk):
                 self.launch(i, self.sets[s % 2][i])
@@ -340,9 +352,10 @@ class StepRunner:
         torch.cuda.synchronize()
         return t0.elapsed_time(t1) / steps
 
-    def time_kernels(self, launches, pool_bytes=512 << 20, graph=True):
-        """Average launch time of each matrix alone: `launches` back-to-back
-        launches rotating over >= pool_bytes of distinct copies of that matrix
+    def time_kernels(self, launches=100, pool_bytes=512 << 20, graph=True, reps=5):
+        """Average launch time of each matrix alone: `reps` x `launches`
+        back-to-back launches rotating over >= pool_bytes of distinct copies
+        of that matrix
         (so every launch streams from HBM, not the Infinity Cache).  With
         `graph` the launches are captured in one HIP graph and replayed, so
         the host's dispatch gaps between back-to-back launches (a few µs each)
@@ -367,20 +380,32 @@ class StepRunner:
                 with torch.cuda.graph(g, stream=self.side):
                     for s in range(launches):
                         self.launch(i, copies[s % len(copies)])
-                g.replay()  # warm
-                torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            with torch.cuda.stream(self.side):
-                e0.record()
+            # replays (or launches) for ~WARM_SECONDS before the timed region,
+            # as for the per-config timings: clocks ramp back up after the
+            # host-side copies
+            t_end = time.perf_counter() + WARM_SECONDS
+            while True:
                 if g is not None:
                     g.replay()
                 else:
                     for s in range(launches):
                         self.launch(i, copies[s % len(copies)])
+                torch.cuda.synchronize()
+                if time.perf_counter() >= t_end:
+                    break
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(self.side):
+                e0.record()
+                for _ in range(reps):
+                    if g is not None:
+                        g.replay()
+                    else:
+                        for s in range(launches):
+                            self.launch(i, copies[s % len(copies)])
                 e1.record()
             torch.cuda.synchronize()
             del g
-            us = e0.elapsed_time(e1) * 1e3 / launches
+            us = e0.elapsed_time(e1) * 1e3 / (reps * launches)
             b = alg_bytes(dt, N, K)
             out[name] = {"us": round(us, 2), "GBs": round(b / us / 1e3, 1),
                          "pct_hbm": round(100 * b / us / 1e3 / PEAK_HBM_GBS, 1),
@@ -447,7 +472,7 @@ def main():
             torch.cuda.synchronize()
             del src, dst
         ms = r.time_steps(args.steps, args.warmup, graph=args.graph)
-        kern = r.time_kernels(max(50, args.steps // 2), graph=args.kernel_launch == "graph")
+        kern = r.time_kernels(graph=args.kernel_launch == "graph")
         results[layout] = (ms, kern)
         r.free()
         del r

@@ -425,8 +425,11 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     }
 
     if (fq::mmqi_supported((int)dtype) && M >= 3 && M <= 8 && K > 0) {
-        // Q4_K, 3..8 tokens: the int8 matrix-core kernel in one pass (M = 2 is
-        // faster on the multi-token batch-1 kernel, M > 8 on the fp16 MFMA path)
+        // Q4_K, 3..8 tokens that the kernels above do not take: three tokens
+        // on weights under 8 MB or rows whose three record sets overflow the
+        // batch-1 kernel's LDS (K = 18944), and 4..8 tokens on more rows than
+        // one mmqs band per CU covers.  The int8 matrix-core kernel runs them
+        // in one pass (M > 8 goes to the fp16 MFMA path)
         const long T = (N + 15) / 16;
         const long G = std::max(1L, std::min<long>(di.cus, T));
         const int tpw = (int)((T + G - 1) / G);
@@ -606,7 +609,7 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     if (!fn || lds > lds_cap) return FQ_ERR_SHAPE;
     int per_cu = 0;
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wg,
-                                                     gguf ? lds + 4 * pcap : lds);
+                                                     gguf ? lds + 4 * (size_t)M * pcap : lds);
     if (e != hipSuccess) return hip_fail(e);
     if (per_cu < 1) return FQ_ERR_SHAPE;
     const int wpb = wg / 64;

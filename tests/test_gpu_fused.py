@@ -143,6 +143,31 @@ def test_fused_errors():
     assert y.shape == (0, N)
 
 
+@pytest.mark.parametrize("dtype", [F.Q6_K, F.Q4_K, F.Q4_0])
+def test_fused_k0_one_token_zeros(dtype):
+    # K = 0 at M = 1: Q6_K (and 8 MB-and-more shapes) are routed to the
+    # one-launch batch-1 kernel, which never runs with no K-slices: y = 0
+    # (silu(0) * 0 for gate+up), written over a NaN-filled output
+    from forge_amd import _lib
+    L = _lib.lib()
+    N = 300
+    w = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(1, dtype=torch.float32, device="cuda")
+    y = torch.full((2 * N,), float("nan"), device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.fq_ffn_up_fused(dtype, x.data_ptr(), w.data_ptr(), w.data_ptr(), y.data_ptr(),
+                             1, 0, N, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y[:N], torch.zeros(N, device="cuda"))
+    assert torch.isnan(y[N:]).all()  # nothing past the N outputs is written
+    y.fill_(float("nan"))
+    assert L.fq_fused_qkv(dtype, x.data_ptr(), w.data_ptr(), w.data_ptr(), w.data_ptr(),
+                          y.data_ptr(), 1, 0, N, 64, 32, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y[:N + 96], torch.zeros(N + 96, device="cuda"))
+    assert torch.isnan(y[N + 96:]).all()
+
+
 def assert_matmul(y, ref, x, w_blocks_list, dtype, K, what):
     deq = np.concatenate([oracle.dequant(dtype, wb, wb.shape[0], K) for wb in w_blocks_list])
     assert_close(y, ref, x, np.array([float(np.max(np.abs(deq)))]), what)

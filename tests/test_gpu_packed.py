@@ -44,6 +44,9 @@ PACKED_SHAPES = [
     ("cfg2-gate", F.Q4_K, 18944, 3584),
     ("cfg2-down", F.Q6_K, 3584, 18944),
     ("cfg2-lm_head", F.Q6_K, 152064, 3584),
+    ("q4_0-7b-up", F.Q4_0, 18944, 3584),
+    ("q4_0-7b-down", F.Q4_0, 3584, 18944),
+    ("q4_0-7b-lm_head", F.Q4_0, 152064, 3584),
     ("q4_1-4096", F.Q4_1, 4096, 4096),
     ("q8_0-3584", F.Q8_0, 3000, 3584),
 ]

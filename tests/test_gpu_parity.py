@@ -100,12 +100,34 @@ CONFIG_GEMV = [
     ("cfg2-gate", F.Q4_K, 18944, 3584),
     ("cfg2-down", F.Q6_K, 3584, 18944),
     ("cfg2-lm_head", F.Q6_K, 152064, 3584),
+    # Qwen2.5-7B in Q4_0, the reference's published decode workload: ffn up,
+    # ffn down (K = 18944) and the >= 64k-row lm_head, on GGUF bytes (the
+    # latter two take the batch-1 kernel's two-units-per-lane forms)
+    ("q4_0-7b-up", F.Q4_0, 18944, 3584),
+    ("q4_0-7b-down", F.Q4_0, 3584, 18944),
+    ("q4_0-7b-lm_head", F.Q4_0, 152064, 3584),
 ]
 
 
 @pytest.mark.parametrize("name,dtype,N,K", CONFIG_GEMV, ids=[c[0] for c in CONFIG_GEMV])
 def test_gemv_configs(name, dtype, N, K):
     check_shape(dtype, N, K, 1, seed=1000 + N + K, what=name)
+
+
+@pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built")
+def test_q4_0_lm_head_vs_reference():
+    # Q4_0 152064 x 3584 lm_head (the reference's output_proj_q4_0_kernel,
+    # cuda_fused.cu:844-922) against the reference's own CPU matmul_transB on
+    # a row subset: the first, a middle and the last 2048 rows
+    N, K = 152064, 3584
+    w = synth.make_weights(F.Q4_0, N, K, 1000 + N + K)
+    x = synth.make_x(1, K, 1001 + N + K)
+    y = run(F.Q4_0, w, x, N, K)
+    for r0 in (0, N // 2 - 1024, N - 2048):
+        ws = np.ascontiguousarray(w[r0:r0 + 2048])
+        yr = oracle.ref_matmul(F.Q4_0, x, ws, 2048, K, threads=16)
+        deq_max = float(np.max(np.abs(oracle.dequant(F.Q4_0, ws, 2048, K))))
+        assert_close(y[:, r0:r0 + 2048], yr, x, np.array([deq_max]), f"rows {r0}+2048 vs reference")
 
 
 @pytest.mark.parametrize("dtype", ALL)
