@@ -441,6 +441,8 @@ def main():
 
     if args.shape:
         from forge_amd import formats as F
+        if args.copy_calibration:
+            copy_calibration(args.copy_calibration)
         names = {f.name.lower(): dt for dt, f in F.FORMATS.items()}
         for spec in args.shape:
             parts = spec.split(":")
@@ -465,12 +467,7 @@ def main():
     for layout in (args.layout, other):
         r = StepRunner(layout, host_w, host_x)
         if layout == args.layout and args.copy_calibration:
-            src = torch.ones(args.copy_calibration << 18, dtype=torch.float32, device="cuda")
-            dst = torch.empty_like(src)
-            for _ in range(3):
-                dst.copy_(src)
-            torch.cuda.synchronize()
-            del src, dst
+            copy_calibration(args.copy_calibration)
         ms = r.time_steps(args.steps, args.warmup, graph=args.graph)
         kern = r.time_kernels(graph=args.kernel_launch == "graph")
         results[layout] = (ms, kern)
@@ -538,6 +535,19 @@ def main():
     if args.formats:
         for line in format_lines(cpu=not args.no_cpu):
             print(json.dumps(line), file=sys.stderr, flush=True)
+
+
+def copy_calibration(mib):
+    """Three device-to-device copies of `mib` MiB: a plain copy kernel of known
+    size, for scaling the HBM byte counters of the same profiler run."""
+    import torch
+    src = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
 
 
 def measured_traffic():

@@ -21,7 +21,7 @@ OBJDIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["fq_dequant.hip", "fq_gemv1.hip", "fq_gemvp.hip", "fq_pack.hip", "fq_mmq.hip",
+SOURCES = ["fq_dequant.hip", "fq_gemv1.hip", "fq_gemvp.hip", "fq_gemvt.hip", "fq_pack.hip", "fq_mmq.hip",
            "fq_mmqi.hip", "fq_mmqs.hip", "fq_mmqp.hip",
            "fq_capi.cpp"]
 

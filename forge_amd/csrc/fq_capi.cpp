@@ -555,6 +555,90 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
                    fixed_cap);
 }
 
+// Batch-1 GEMV over the tiled aligned layout, one row per lane
+// (fq_gemvt.hip; every matrix involved satisfies packed_tiled()).  N output
+// rows (mode 1: rows of each of the two matrices).  W waves per work-group
+// (one K range each), 16 / W work-groups per CU, the tiles dealt out in turn
+// so every work-group gets the same number within one; W shrinks until a
+// work-group's tiles fit its LDS (gemvt_max_tiles()).
+int run_gemvt(uint32_t dtype, const float* x, const void* w, const void* w2, const void* w3,
+              int n1, int n2, int mode, const float* bias, int64_t bias_len, float* y, int K,
+              int N, hipStream_t st, const DevInfo& di) {
+    const int U = fq::gemvt_units((int)dtype, K);
+    if (U % 4 != 0) return FQ_ERR_SHAPE;
+    const int GR = U / 4;
+    const int TRW = fq::gemvt_tile_rows();
+    const long tiles = mode == 2 ? (long)(n1 + TRW - 1) / TRW + (n2 + TRW - 1) / TRW +
+                                       (N - n1 - n2 + TRW - 1) / TRW
+                                 : (long)(N + TRW - 1) / TRW;
+    if (tiles > INT32_MAX / TRW) return FQ_ERR_SHAPE;
+    // the kernel addresses each matrix through a 32-bit buffer offset
+    const int64_t RB = fq::packed_row_bytes((int)dtype, K);
+    if ((int64_t)(mode == 2 ? std::max(n1, std::max(n2, N - n1 - n2)) : N) * RB >= ((int64_t)1 << 32))
+        return FQ_ERR_SHAPE;
+    const int WM = fq::gemvt_max_waves(), ntmax = fq::gemvt_max_tiles();
+    const int maxrec = fq::gemvt_max_records(), RBY = fq::gemvt_record_bytes();
+    const int NV = mode == 1 ? 2 : 1;
+    const size_t cu_lds = std::min<size_t>(di.lds, 160 * 1024);
+    auto recs_of = [&](int w) { return ((GR + w - 1) / w) * 4; };
+    auto lds_of = [&](int w, long nt) {
+        return (size_t)w * recs_of(w) * RBY + (size_t)nt * NV * w * 64 * 4;
+    };
+    // the fewest waves per work-group (more work-groups per CU, the same 16
+    // waves) whose records fit and whose tiles stay within gemvt_max_tiles()
+    // and the CU's LDS
+    int W = 0;
+    long GT = 0;
+    for (int w = std::min(WM, GR); w >= 1; w = w > 1 ? std::max(1, w / 2) : 0) {
+        if (recs_of(w) > maxrec) break;
+        const int wpc = std::max(1, WM / w);
+        const long gt = std::min<long>(tiles, (long)di.cus * wpc);
+        const long nt = (tiles + gt - 1) / gt;
+        if (nt <= ntmax && lds_of(w, nt) * wpc <= cu_lds) {
+            W = w;
+            GT = gt;
+            if (nt * 2 > ntmax) break;  // fewer waves would not fit the next halving
+        } else if (W) {
+            break;
+        }
+    }
+    if (!W) {  // very long rows or very many tiles: the smallest fitting W, more work-groups
+        W = std::min(WM, GR);
+        while (W < WM && recs_of(W) > maxrec) W = std::min(WM, 2 * W);
+        if (recs_of(W) > maxrec) return FQ_ERR_SHAPE;
+        const size_t fixed = lds_of(W, 0);
+        if (fixed >= cu_lds) return FQ_ERR_SHAPE;
+        const long ntcap = std::max<long>(1, std::min<long>(ntmax, (long)((cu_lds - fixed) / ((size_t)NV * W * 64 * 4))));
+        GT = (tiles + ntcap - 1) / ntcap;
+    }
+    const int recs = recs_of(W);
+    const int nt_max = (int)((tiles + GT - 1) / GT);
+    const size_t lds = lds_of(W, nt_max);
+    if (lds > cu_lds) return FQ_ERR_SHAPE;
+    const void* fn = fq::gemvt_kernel_fn((int)dtype, mode);
+    if (!fn) return FQ_ERR_DTYPE;
+    fq::TArgs a{};
+    a.x = x;
+    a.w = static_cast<const uint8_t*>(w);
+    a.w2 = static_cast<const uint8_t*>(w2);
+    a.w3 = static_cast<const uint8_t*>(w3);
+    a.n1 = n1;
+    a.n2 = n2;
+    a.y = y;
+    a.bias = bias;
+    a.bias_len = bias ? bias_len : 0;
+    a.mode = mode;
+    a.N = N;
+    a.K = K;
+    a.U = U;
+    a.GR = GR;
+    a.recs = recs;
+    a.T = (int)tiles;
+    a.row_bytes = RB;
+    const hipError_t e = fq::launch_gemvt(fn, a, (int)GT, W, lds, st);
+    return e == hipSuccess ? FQ_OK : hip_fail(e);
+}
+
 // Batch-1 GEMV over packed rows.  mode 0: y = x . w (+ bias).  mode 1 (fused
 // gate/up): y[n] = silu(x . w[n]) * (x . w2[n]), run as one GEMV over 2 N
 // interleaved rows.  mode 2 (fused QKV): y = [x . w | x . w2 | x . w3] with
@@ -585,6 +669,29 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
         if (bias) return FQ_ERR_SHAPE;
         e = fq::launch_zero(reinterpret_cast<uint32_t*>(y), (size_t)N, di.cus, st);
         return e == hipSuccess ? FQ_OK : hip_fail(e);
+    }
+    if (!gguf) {
+        // the arrangement of each packed matrix follows from its rows
+        const int nr[3] = {mode == 2 ? n1 : N, mode == 2 ? n2 : N, mode == 2 ? N - n1 - n2 : N};
+        const int nm = mode == 0 ? 1 : mode == 1 ? 2 : 3;
+        int tiled = 0;
+        for (int i = 0; i < nm; ++i) tiled += fq::packed_tiled((int)dtype, nr[i]) ? 1 : 0;
+        if (tiled == nm)
+            return run_gemvt(dtype, x, w_packed, w2_packed, w3_packed, n1, n2, mode, bias,
+                             bias_len, y, K, N, st, di);
+        if (tiled > 0) {  // fused QKV over both arrangements: one GEMV per matrix
+            const void* ws[3] = {w_packed, w2_packed, w3_packed};
+            int off = 0;
+            for (int i = 0; i < 3; ++i) {
+                if (nr[i] > 0) {
+                    const int rc = packed_gemv(dtype, x, ws[i], nullptr, nullptr, 0, 0, 0, nullptr,
+                                               0, y + off, K, nr[i], st, false);
+                    if (rc != FQ_OK) return rc;
+                }
+                off += nr[i];
+            }
+            return FQ_OK;
+        }
     }
     int units = 0, records = 0;
     fq::gemvp_geometry((int)dtype, K, &units, &records);

@@ -47,6 +47,32 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
 // forms, one token, no bias
 const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
                             int* wg, int* nl, int rows, int tokens = 1, int mode = 0);
+// batch-1 GEMV over the tiled aligned layout (fq_gemvt.hip; Q4_0, Q4_1, Q8_0
+// matrices for which packed_tiled() holds), one row per lane
+struct TArgs {
+    const float* x;             // [K]
+    const uint8_t *w, *w2, *w3; // packed matrices (w2: up for the fused gate/up; w2, w3: K, V)
+    int n1, n2;                 // fused QKV: rows of Q and K
+    float* y;                   // [N]
+    const float* bias;          // optional row vector, bias[n] for n < bias_len
+    int64_t bias_len;
+    int mode;                   // 0 plain, 1 fused gate/up (N rows each), 2 fused QKV
+    int N, K;                   // output rows; K
+    int U;                      // blocks per row (gemvt_units)
+    int GR;                     // steps of four blocks per row (U / 4)
+    int T;                      // tiles
+    int recs;                   // activation records in each wave's LDS area
+    int64_t row_bytes;          // packed row bytes
+};
+int gemvt_units(int dtype, int K);
+int gemvt_max_records();    // per wave
+int gemvt_max_tiles();      // per work-group
+int gemvt_max_waves();      // per work-group
+int gemvt_tile_rows();
+int gemvt_record_bytes();
+const void* gemvt_kernel_fn(int dtype, int mode);
+hipError_t launch_gemvt(const void* fn, const TArgs& a, int grid, int waves, size_t lds,
+                        hipStream_t st);
 hipError_t launch_pack(int dtype, const uint8_t* src, uint8_t* dst, int N, int K, bool pack,
                        int grid, hipStream_t st);
 hipError_t launch_zero(uint32_t* p, size_t n, int grid, hipStream_t st);

@@ -2,12 +2,25 @@
 //
 // GGUF rows are arrays of 18/20/34/144/210-byte blocks, so most blocks sit at
 // 2-byte alignment.  The packed layout holds exactly the same bytes per row,
-// rearranged into "planes": the 16-byte pieces a GEMV lane reads for lane
-// unit v sit at plane + 16 v, so one load instruction of a wave reads 1 KiB
-// of contiguous bytes, and the per-block scales form small dense arrays after
-// the planes.  Rows stay contiguous; the row stride is packed_row_bytes(K), a
-// multiple of 16, and K must be a multiple of 256.  Dequantizing packed bytes
-// gives exactly the values of the original blocks (the bytes are only moved).
+// rearranged into "planes" (the table below, in 16-byte pieces; the per-block
+// scales form small dense arrays after the quant planes).  A row takes
+// packed_row_bytes(K) bytes, a multiple of 16, and K must be a multiple of
+// 256.  N rows take N packed_row_bytes(K) bytes, arranged one of two ways
+// (packed_tiled() decides from the format and N; fq_pack_weights and the
+// GEMVs apply the same rule):
+//  - row-major: row n at n packed_row_bytes(K), its pieces in plane order;
+//    a batch-1 lane reads piece v of a row, so a wave's load moves 1 KiB of
+//    one row (fq_gemvp.hip);
+//  - 16-row tiles (Q4_0, Q4_1, Q8_0 with at least TILED_MIN_ROWS rows):
+//    tile t starts at byte 16 t packed_row_bytes(K), and within a tile of R
+//    rows (the last tile holds the N mod 16 remaining rows) piece J of row r
+//    sits at (J R + r) 16.  Pieces J .. J+3 of the tile's rows are one
+//    contiguous 1 KiB run, read by a wave whose 64 lanes work on 16 rows
+//    times four pieces (fq_gemvt.hip).
+// Dequantizing packed bytes gives exactly the values of the original blocks
+// (the bytes are only moved).
+//
+// The per-row plane table (byte offsets within a row's pieces):
 //
 //   Q4_0  [qs: U x 16][d: U x 2, padded to 16]                  U = K/32
 //   Q4_1  [qs: U x 16][d,m: U x 4]
@@ -26,6 +39,16 @@
 namespace fq {
 
 __host__ __device__ inline int64_t pad16(int64_t b) { return (b + 15) & ~(int64_t)15; }
+
+// The tiled arrangement: the one-row-per-lane kernel (fq_gemvt.hip) against
+// the one-row-per-step kernel (fq_gemvp.hip), 152064 x 3584, M = 1: Q4_0 53.5
+// against 67.8 us, Q4_1 55.9 / 70.4, Q8_0 88.3 / 97.9; the superblock
+// formats do not gain (Q4_K 55.2 / 55.0, Q6_K 77.4 / 69.1), nor do matrices
+// of fewer rows (Q4_0 18944 x 3584: 14.4 / 11.0).
+constexpr int64_t TILED_MIN_ROWS = 65536;
+__host__ __device__ inline bool packed_tiled(int dtype, int64_t N) {
+    return (dtype == 2 || dtype == 3 || dtype == 7) && N >= TILED_MIN_ROWS;
+}
 
 // Packed row stride in bytes (0 when the format has no packed form).
 __host__ __device__ inline int64_t packed_row_bytes(int dtype, int64_t K) {
