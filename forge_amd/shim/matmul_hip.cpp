@@ -122,10 +122,13 @@ TensorPtr ffn_up_fused_device(const TensorPtr& input, const TensorPtr& w1, const
 }
 
 // [M, N1 + N2] = [a . b1^T | a . b2^T].  One dtype: one fq_fused_qkv call
-// (a single activation staging at M = 1); two dtypes (a Q4_K_M model's Q4_K
-// key and Q6_K value projections): two matmuls whose rows are interleaved into
-// the output with strided device copies, as the reference's CUDA branch does
-// with per-row cudaMemcpyAsync.
+// (a single activation staging at M = 1).  Two dtypes (a Q4_K_M model's Q4_K
+// key and Q6_K value projections): two matmuls.  At M = 1 each writes its
+// slice of the output row directly; for more rows each writes a stream-ordered
+// temporary (hipMallocAsync) whose rows a strided device copy interleaves
+// into the output, as the reference's CUDA branch does with per-row
+// cudaMemcpyAsync, and the temporary is released in stream order
+// (hipFreeAsync): nothing waits on the host.
 TensorPtr matmul_transB_dual_device(const TensorPtr& a, const TensorPtr& b1,
                                     const TensorPtr& b2) {
     need_2d("matmul_transB_dual", {&a, &b1, &b2});
@@ -144,28 +147,35 @@ TensorPtr matmul_transB_dual_device(const TensorPtr& a, const TensorPtr& b1,
                  "matmul_transB_dual");
         return out;
     }
-    const TensorPtr parts[2] = {fp32_on(a->device(), M, N1), fp32_on(a->device(), M, N2)};
     const TensorPtr* ws[2] = {&b1, &b2};
     const int ns[2] = {N1, N2};
+    auto hip_check = [](hipError_t e, const char* what) {
+        if (e != hipSuccess)
+            throw std::runtime_error(std::string("matmul_transB_dual: ") + what + " failed (" +
+                                     std::to_string(static_cast<int>(e)) + ")");
+    };
     int off = 0;
     for (int i = 0; i < 2; ++i) {
-        fq_check(fq_matmul_transB(static_cast<uint32_t>((*ws[i])->dtype()), x, (*ws[i])->data(),
-                                  nullptr, 0, 0, static_cast<float*>(parts[i]->data()), M, K,
-                                  ns[i], nullptr),
-                 "matmul_transB_dual");
-        if (ns[i] > 0 && M > 0) {
-            const hipError_t e = hipMemcpy2DAsync(
-                y + off, sizeof(float) * (N1 + N2), parts[i]->data(), sizeof(float) * ns[i],
-                sizeof(float) * ns[i], M, hipMemcpyDeviceToDevice, nullptr);
-            if (e != hipSuccess)
-                throw std::runtime_error("matmul_transB_dual: hipMemcpy2DAsync failed (" +
-                                         std::to_string(static_cast<int>(e)) + ")");
+        const uint32_t dt = static_cast<uint32_t>((*ws[i])->dtype());
+        if (M == 1 || ns[i] == 0) {
+            fq_check(fq_matmul_transB(dt, x, (*ws[i])->data(), nullptr, 0, 0, y + off, M, K, ns[i],
+                                      nullptr),
+                     "matmul_transB_dual");
+        } else if (M > 0) {
+            void* part = nullptr;
+            hip_check(hipMallocAsync(&part, sizeof(float) * (size_t)M * ns[i], nullptr),
+                      "hipMallocAsync");
+            fq_check(fq_matmul_transB(dt, x, (*ws[i])->data(), nullptr, 0, 0,
+                                      static_cast<float*>(part), M, K, ns[i], nullptr),
+                     "matmul_transB_dual");
+            hip_check(hipMemcpy2DAsync(y + off, sizeof(float) * (N1 + N2), part,
+                                       sizeof(float) * ns[i], sizeof(float) * ns[i], M,
+                                       hipMemcpyDeviceToDevice, nullptr),
+                      "hipMemcpy2DAsync");
+            hip_check(hipFreeAsync(part, nullptr), "hipFreeAsync");
         }
         off += ns[i];
     }
-    // the parts must outlive the copies queued on the null stream
-    if (hipStreamSynchronize(nullptr) != hipSuccess)
-        throw std::runtime_error("matmul_transB_dual: stream synchronisation failed");
     return out;
 }
 
