@@ -64,6 +64,9 @@ def parse():
     p.add_argument("--shape", action="append", default=[], metavar="DTYPE:NxK[:M]",
                    help="only time these shapes (e.g. q4_0:152064x3584:1), GGUF and, for "
                         "M = 1, aligned layout; one JSON line each on stdout")
+    p.add_argument("--fused", action="append", default=[], metavar="DTYPE:NxK",
+                   help="only time the fused gate/up (aligned, two GEMVs, GGUF) at these "
+                        "shapes; one JSON line each on stdout")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--warm-seconds", type=float, default=0.2,
                    help="graph replays before each per-config timing (clock ramp)")
@@ -439,11 +442,15 @@ def main():
         sys.exit(1)
     torch.cuda.set_device(0)
 
-    if args.shape:
+    if args.shape or args.fused:
         from forge_amd import formats as F
         if args.copy_calibration:
             copy_calibration(args.copy_calibration)
         names = {f.name.lower(): dt for dt, f in F.FORMATS.items()}
+        for spec in args.fused:
+            parts = spec.split(":")
+            N, K = (int(v) for v in parts[1].lower().split("x"))
+            print(json.dumps(time_fused(spec, names[parts[0].lower()], N, K)), flush=True)
         for spec in args.shape:
             parts = spec.split(":")
             dt = names[parts[0].lower()]

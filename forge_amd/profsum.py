@@ -97,6 +97,87 @@ def counters(path: str, match: str = ""):
     return rows
 
 
+def _agg(path: str):
+    """{(short kernel name, grid, LDS): {counter: mean per dispatch}} of a --pmc CSV."""
+    agg = collections.OrderedDict()
+    for r in csv.DictReader(open(path)):
+        key = (short(r["Kernel_Name"]), int(r["Grid_Size"]), int(r["LDS_Block_Size"]))
+        d = agg.setdefault(key, {})
+        tot, n = d.get(r["Counter_Name"], (0.0, 0))
+        d[r["Counter_Name"]] = (tot + float(r["Counter_Value"]), n + 1)
+    return {k: {c: t / n for c, (t, n) in d.items()} for k, d in agg.items()}
+
+
+def shape_table(runs, copy_mib: float, match: str):
+    """One row per (shape, kernel) from per-shape --pmc runs.
+
+    runs: "SPEC=DIR" items, SPEC = DTYPE:NxK[:M] (the bench --shape spec) or
+    fused:DTYPE:NxK, DIR holding that shape's pass CSVs (*_counter_collection.csv,
+    any number of passes; the FETCH_SIZE / WRITE_SIZE passes must include the
+    --copy-calibration copy).  Derived columns:
+      HBM/alg   (FETCH_SIZE + WRITE_SIZE bytes, each scaled by the copy's
+                reading) / algorithmic bytes of the call
+      VALU/B    SQ_INSTS_VALU (wave instructions) per weight byte
+      VALU%     SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES
+      wait%     SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (waves waiting on a dependency)
+      TA%       TA_TA_BUSY_sum / (GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs): the
+                address unit's busy share
+      MFMA%     SQ_VALU_MFMA_BUSY_CYCLES / (cycles x 1024 SIMDs)
+      cycles    GRBM_GUI_ACTIVE / 8 (GPU cycles per XCD for the dispatch,
+                including the profiler's per-dispatch overhead)
+    Runtime and torch kernels (the copy calibration, fills) are left out.
+    """
+    import glob
+    import os
+    from forge_amd.formats import FORMATS
+    names = {f.name.lower(): dt for dt, f in FORMATS.items()}
+    print("| shape | kernel | grid | cycles | HBM/alg | VALU/B | VALU% | wait% | TA% | MFMA% |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for item in runs:
+        spec, d = item.split("=", 1)
+        parts = spec.split(":")
+        fused = parts[0] == "fused"
+        if fused:
+            parts = parts[1:]
+        dt = names[parts[0].lower()]
+        N, K = (int(v) for v in parts[1].lower().split("x"))
+        M = int(parts[2]) if len(parts) > 2 else 1
+        f = FORMATS[dt]
+        wbytes = f.matrix_bytes(N, K) * (2 if fused else 1)
+        alg = wbytes + 4 * M * K + 4 * M * N
+        merged = {}
+        kib = copy_mib * 1024.0
+        scale = {}
+        for path in sorted(glob.glob(os.path.join(d, "*_counter_collection.csv"))):
+            for k, c in _agg(path).items():
+                merged.setdefault(k, {}).update(c)
+            for r in csv.DictReader(open(path)):
+                if "copy" in r["Kernel_Name"].lower() and r["Counter_Name"] in ("FETCH_SIZE", "WRITE_SIZE"):
+                    scale[r["Counter_Name"]] = max(scale.get(r["Counter_Name"], 0.0),
+                                                   float(r["Counter_Value"]))
+        for (name, grid, lds), c in merged.items():
+            if match not in name or name.startswith(("at::", "__amd")):
+                continue
+            hbm = ""
+            if "FETCH_SIZE" in c and "WRITE_SIZE" in c and scale.get("FETCH_SIZE") and scale.get("WRITE_SIZE"):
+                b = (c["FETCH_SIZE"] / (scale["FETCH_SIZE"] / kib) +
+                     c["WRITE_SIZE"] / (scale["WRITE_SIZE"] / kib)) * 1024.0
+                hbm = f"{b / alg:.3f}"
+            cyc = c.get("GRBM_GUI_ACTIVE", 0.0) / 8.0
+            def ratio(a, b, pct=True):
+                if a in c and b in c and c[b] > 0:
+                    return f"{100 * c[a] / c[b]:.0f}" if pct else f"{c[a] / c[b]:.3f}"
+                return ""
+            valub = f"{c['SQ_INSTS_VALU'] / wbytes:.4f}" if "SQ_INSTS_VALU" in c else ""
+            ta = (f"{100 * c['TA_TA_BUSY_sum'] / (cyc * 256):.0f}"
+                  if "TA_TA_BUSY_sum" in c and cyc > 0 else "")
+            mf = (f"{100 * c['SQ_VALU_MFMA_BUSY_CYCLES'] / (cyc * 1024):.0f}"
+                  if "SQ_VALU_MFMA_BUSY_CYCLES" in c and cyc > 0 else "")
+            print(f"| {spec} | `{name}` | {grid} | {cyc:.0f} | {hbm} | "
+                  f"{valub} | {ratio('SQ_ACTIVE_INST_VALU', 'SQ_WAVE_CYCLES')} | "
+                  f"{ratio('SQ_WAIT_INST_ANY', 'SQ_WAVE_CYCLES')} | {ta} | {mf} |")
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--counters", metavar="COUNTER_CSV",
@@ -109,7 +190,12 @@ def main():
     p.add_argument("--kernel", default="gemvp_kernel<13")
     p.add_argument("--grid", type=int, default=0)
     p.add_argument("--lds", type=int, default=0)
+    p.add_argument("--shapes", nargs="+", metavar="SPEC=DIR",
+                   help="per-shape --pmc run directories: one table of derived ratios")
     a = p.parse_args()
+    if a.shapes:
+        shape_table(a.shapes, a.copy_mib, a.match)
+        return
     if a.counters:
         for r in counters(a.counters, a.match):
             print(f"- `{short(r.pop('kernel'))}` grid {r.pop('grid')} LDS {r.pop('lds')} "
