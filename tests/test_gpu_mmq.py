@@ -106,3 +106,24 @@ def test_q4k_small_batch_int8_path(M, N, K):
     y = check(F.Q4_K, N, K, x, seed=K + M, what=f"q4_k M={M} {N}x{K}")
     y2 = check(F.Q4_K, N, K, x, seed=K + M, what="again")
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))  # deterministic
+
+
+@pytest.mark.parametrize("M", [4, 7, 16])
+@pytest.mark.parametrize("N,K", [(333, 1024), (2000, 4096), (4100, 512)])
+def test_q4k_band_kernel(M, N, K):
+    # Q4_K, 4 <= M <= 16 on at most one band of rows per CU: the band kernel
+    # (fq_mmqs.hip) makes the token operands itself from x; tokens past M
+    # read as zeros.  Chunk magnitudes from 1e-20 to 1e20 and an all-zero
+    # chunk exercise its per-(token, chunk) exponents.
+    x = synth.make_x(M, K, seed=N + M)
+    scales = 10.0 ** np.linspace(-20, 20, K // 64)
+    x = (x.reshape(M, K // 64, 64) * scales[None, :, None].astype(np.float32)).reshape(M, K)
+    x[M - 1, 64:128] = 0.0
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = check(F.Q4_K, N, K, x, seed=K + M, what=f"q4_k band M={M} {N}x{K}")
+    y2 = run(F.Q4_K, synth.make_weights(F.Q4_K, N, K, K + M), x, N, K)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))  # deterministic
+    # the first four tokens alone give the same bits
+    if M > 4:
+        y4 = run(F.Q4_K, synth.make_weights(F.Q4_K, N, K, K + M), x[:4], N, K)
+        assert np.array_equal(y[:4].view(np.uint32), y4.view(np.uint32))
