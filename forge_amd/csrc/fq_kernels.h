@@ -89,7 +89,6 @@ const void* mmqi_kernel_fn(int mt_needed, bool bias, int K, int tiles_per_wg, in
 // M > 1 on MFMA (fq_mmq.hip)
 struct MmqArgs {
     const uint8_t* w;     // GGUF rows
-    const float* x;       // [M][K] activations (mmqs: read directly)
     const void* xop;      // fp16 token operands, [Tp][NC][2048]
     const float* xsum;    // [Tp][NC][64] sub-block sums of the scaled activations
     const int* ex;        // [Tp][NC][16] power-of-two exponent per (token, chunk)
@@ -106,9 +105,9 @@ hipError_t launch_xprep(int dtype, const float* x, int M, int K, int NC, _Float1
                         float* xsum, int* ex, hipStream_t st);
 hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, int splits,
                       hipStream_t st);
-// 4..16 tokens on the fp16 matrix cores, weights streamed once (fq_mmqs.hip):
-// a.x (M * K * 4 bytes below 2^31) made into token operands in the kernel,
-// bands of rows_per_wg rows (at most 16 mmqs_max_tiles()) per work-group
+// 2..16 tokens on the fp16 matrix cores, weights streamed once (fq_mmqs.hip):
+// the token operands of launch_xprep (one token tile), bands of rows_per_wg
+// rows (at most 16 mmqs_max_tiles()) per work-group
 bool mmqs_supported(int dtype);
 int mmqs_max_tiles();
 hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hipStream_t st);

@@ -15,16 +15,15 @@
 //         sub-block: x_hi and x_lo accumulate into the same fp32 D_s;
 //   A_s: exact fp16 quants (lane 16 q + r: row r, elements 8 q .. 8 q + 7 in
 //        the slot order of fq_mfma16.h);
-//   B_s: the token operands, made by the wave from x as it loads it (prep()
-//        below, the same values as xprep_kernel of fq_mmq.hip): x of the
-//        chunk scaled by 2^-e (one exponent per token and chunk), split into
-//        fp16 hi + lo (22 significant bits), in the same slot order;
+//   B_s: the token operands of xprep_kernel (fq_mmq.hip): x of the chunk
+//        scaled by 2^-e (one exponent per token and chunk), split into fp16
+//        hi + lo (22 significant bits), in the same slot order;
 //
 // and adds  2^e (A_0 D_0 + A_1 D_1 + B_0 S_0 + B_1 S_1)  to its accumulators,
 // with (A_s, B_s) the sub-block's affine pair of the format (Q4_K: d sc and
 // -dmin m, matmul.cpp:340-377) and S_s the scaled sub-block sums of x.  The
-// activations of a super-block are loaded once per wave (one super-block
-// ahead, with its weights) and reused by every tile of the band.
+// token operands of a chunk are loaded once per wave (one chunk ahead) and
+// reused by every tile of the band.
 //
 // The scale coefficients of a row come from its super-block header; D's lanes
 // hold rows 4 q' .. 4 q' + 3 of token c, so the coefficients go through a
@@ -43,6 +42,10 @@
 
 namespace fq {
 namespace {
+
+constexpr int KC = 64;      // K elements per chunk (as xprep_kernel)
+constexpr int XOP = 2048;   // halves per (token tile, chunk)
+constexpr int XSUM = 64;    // sub-block sums per (token tile, chunk)
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -83,65 +86,6 @@ struct Band<Q4_K> {
 
 constexpr int NPL = 3;  // 16-byte pieces per lane per panel (144 / 64, rounded up)
 
-// The activations are raw buffer loads: a token past M lies beyond the
-// buffer's range and reads as zeros (no memory access).
-typedef __amdgpu_buffer_rsrc_t Buf;
-typedef float fq_f32x4v __attribute__((ext_vector_type(4)));
-
-// Token operands of one chunk for lane (q, c): token c's elements
-// 64 ch + 8 q + [0, 8) (sub-block 0) and 64 ch + 32 + 8 q + [0, 8)
-// (sub-block 1), as loaded (v[0..1], v[2..3]), become
-//   e    = ilogb(max |x| over the token's 64 chunk elements) - 14 (0 for an
-//          all-zero chunk), so that x 2^-e lies in [2^14, 2^15);
-//   h, l = fp16 hi + lo of x 2^-e in slot order (fq_mfma16.h);
-//   S    = the sub-block sums of x 2^-e: each quad (x0 + x1) + (x2 + x3),
-//          then pairs of quads, then across the lanes q ^ 1 and q ^ 2 -- the
-//          same fixed tree for every lane, so all four lanes of a token hold
-//          the same sums.
-struct Xop {
-    h8 h0, l0, h1, l1;
-    float p2, S0, S1;
-};
-
-__device__ __forceinline__ Xop prep(const fq_f32x4v (&v)[4]) {
-    float w[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        w[4 * i] = v[i].x;
-        w[4 * i + 1] = v[i].y;
-        w[4 * i + 2] = v[i].z;
-        w[4 * i + 3] = v[i].w;
-    }
-    float mx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(w[i]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    int e = 0;
-    if (mx > 0.0f && mx <= 3.0e38f) e = ilogbf(mx) - 14;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = ldexpf(w[i], -e);
-    Xop o;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float t0 = w[slot_elem(i)], t1 = w[8 + slot_elem(i)];
-        o.h0[i] = (_Float16)t0;
-        o.l0[i] = (_Float16)(t0 - (float)o.h0[i]);
-        o.h1[i] = (_Float16)t1;
-        o.l1[i] = (_Float16)(t1 - (float)o.h1[i]);
-    }
-    float s0 = ((w[0] + w[1]) + (w[2] + w[3])) + ((w[4] + w[5]) + (w[6] + w[7]));
-    float s1 = ((w[8] + w[9]) + (w[10] + w[11])) + ((w[12] + w[13]) + (w[14] + w[15]));
-    s0 += __shfl_xor(s0, 16, 64);
-    s1 += __shfl_xor(s1, 16, 64);
-    s0 += __shfl_xor(s0, 32, 64);
-    s1 += __shfl_xor(s1, 32, 64);
-    o.p2 = __builtin_amdgcn_ldexpf(1.0f, e);
-    o.S0 = s0;
-    o.S1 = s1;
-    return o;
-}
-
 template <int F, int TW, int WG, bool BIAS>
 __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
     using B = Band<F>;
@@ -175,6 +119,7 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
 #pragma unroll
     for (int t = 0; t < TW; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    const fq_u32x4* xop = reinterpret_cast<const fq_u32x4*>(a.xop);
     auto load_panels = [&](int sb, fq_u32x4 (&pv)[TW][NPL]) {
 #pragma unroll
         for (int t = 0; t < TW; ++t)
@@ -187,28 +132,32 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
             }
     };
 
-    // the activations of a super-block: chunk g of it, quarter i = the four
-    // elements 64 g + 32 (i / 2) + 8 q + 4 (i % 2) of token c
-    const Buf xb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), (short)0,
-                                                     a.M * a.K * 4, 0x00020000);
-    const uint32_t xo0 = c < a.M ? (uint32_t)(c * a.K + 8 * q) * 4u : 0x80000000u;
-    auto load_x1 = [&](int sb, int g, fq_f32x4v (&xg)[4]) {
+    auto load_x = [&](int ch, fq_u32x4 (&xv)[4]) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            xg[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                xb, xo0 + (uint32_t)(sb * B::SBK + 64 * g + 32 * (i >> 1) + 4 * (i & 1)) * 4u, 0,
-                0);
+        for (int i = 0; i < 4; ++i) xv[i] = xop[(size_t)ch * (XOP / 8) + 64 * i + lane];
     };
 
-    // Each pass over a super-block issues the next one's loads (weights, then
-    // activations chunk by chunk as their registers free up), so one wait per
-    // super-block covers both.
+    // exponent and the two sub-block sums of token c in chunk ch
+    struct Xs {
+        int e;
+        float S0, S1;
+    };
+    auto load_s = [&](int ch) {
+        return Xs{a.ex[(size_t)ch * 16 + c], a.xsum[(size_t)ch * XSUM + c],
+                  a.xsum[(size_t)ch * XSUM + 16 + c]};
+    };
+
+    // Token operands are prefetched one chunk ahead.  (Loading all four
+    // chunks of the next super-block ahead of its panel loads, so that no
+    // short L2 load queues behind a long HBM load in the in-order vector
+    // memory counter, needs about 250 VGPRs and measured slower.)
     int sb = wave;
     fq_u32x4 pv[TW][NPL];
-    fq_f32x4v xv[4][4];
+    fq_u32x4 xv[4];  // the token operands of the chunk computed next
+    Xs xs{0, 0.0f, 0.0f};
     if (sb < nsb) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) load_x1(sb, g, xv[g]);
+        load_x(4 * sb, xv);
+        xs = load_s(4 * sb);
         load_panels(sb, pv);
     }
     while (sb < nsb) {  // wave-uniform
@@ -218,8 +167,8 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
             for (int i = 0; i < NPL; ++i)
                 if (lane + 64 * i < B::PIECES)
                     *reinterpret_cast<fq_u32x4*>(&panels[wave][t][16 * (lane + 64 * i)]) = pv[t][i];
-        const int nx = sb + W, sn = min(nx, nsb - 1);
-        load_panels(sn, pv);  // the next super-block's loads (clamped)
+        const int nx = sb + W;
+        load_panels(min(nx, nsb - 1), pv);  // the next super-block's loads (clamped)
         // the super-block's coefficients: lane (r, q) decodes pair q of row r
         // (the wave's own LDS writes precede its reads: in order)
 #pragma unroll
@@ -234,22 +183,27 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
         }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            // chunk g's token operands; its registers then take the next
-            // super-block's chunk g (behind the weight loads above: both are
-            // waited for at the next super-block's top)
-            const Xop xo = prep(xv[g]);
-            load_x1(sn, g, xv[g]);
-            const float S0 = xo.S0, S1 = xo.S1, p2 = xo.p2;
+            const int ch = 4 * sb + g;
+            // the following chunk's token operands (the next super-block's
+            // first after the last), in flight while this chunk computes
+            fq_u32x4 xn[4];
+            const int cn = g < 3 ? ch + 1 : 4 * min(nx, nsb - 1);
+            load_x(cn, xn);
+            const Xs xsn = load_s(cn);
+            const float S0 = xs.S0, S1 = xs.S1;
+            const float p2 = __builtin_amdgcn_ldexpf(1.0f, xs.e);
+            const h8 xh0 = __builtin_bit_cast(h8, xv[0]), xl0 = __builtin_bit_cast(h8, xv[1]);
+            const h8 xh1 = __builtin_bit_cast(h8, xv[2]), xl1 = __builtin_bit_cast(h8, xv[3]);
 #pragma unroll
             for (int t = 0; t < TW; ++t) {
                 if (t < ntl) {  // wave-uniform
                     h8 a0, a1;
                     B::operands(panels[wave][t], g, r, q, a0, a1);
                     const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xo.h0, z, 0, 0, 0);
-                    d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xo.l0, d0, 0, 0, 0);
-                    f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xo.h1, z, 0, 0, 0);
-                    d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xo.l1, d1, 0, 0, 0);
+                    f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xh0, z, 0, 0, 0);
+                    d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xl0, d0, 0, 0, 0);
+                    f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xh1, z, 0, 0, 0);
+                    d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xl1, d1, 0, 0, 0);
                     const float4 A0 = *reinterpret_cast<const float4*>(&coef[wave][t][g][0][4 * q]);
                     const float4 A1 = *reinterpret_cast<const float4*>(&coef[wave][t][g][1][4 * q]);
                     const float4 B0 = *reinterpret_cast<const float4*>(&coef[wave][t][g][2][4 * q]);
@@ -268,6 +222,9 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
                     }
                 }
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[i] = xn[i];
+            xs = xsn;
         }
         sb = nx;
     }

@@ -112,9 +112,9 @@ def test_q4k_small_batch_int8_path(M, N, K):
 @pytest.mark.parametrize("N,K", [(333, 1024), (2000, 4096), (4100, 512)])
 def test_q4k_band_kernel(M, N, K):
     # Q4_K, 4 <= M <= 16 on at most one band of rows per CU: the band kernel
-    # (fq_mmqs.hip) makes the token operands itself from x; tokens past M
-    # read as zeros.  Chunk magnitudes from 1e-20 to 1e20 and an all-zero
-    # chunk exercise its per-(token, chunk) exponents.
+    # (fq_mmqs.hip) on the token operands of xprep_kernel; tokens past M are
+    # padding.  Chunk magnitudes from 1e-20 to 1e20 and an all-zero chunk
+    # exercise the per-(token, chunk) exponents.
     x = synth.make_x(M, K, seed=N + M)
     scales = 10.0 ** np.linspace(-20, 20, K // 64)
     x = (x.reshape(M, K // 64, 64) * scales[None, :, None].astype(np.float32)).reshape(M, K)
