@@ -169,6 +169,28 @@ MmqPlan plan_mmq(int M, int K, int N, int cus) {
     return p;
 }
 
+// Rows per band and K-splits of the small-batch band kernel.  Short rows:
+// bands of up to four 16-row tiles, as few rows per band as fill every CU,
+// unsplit.  Long rows (32 super-blocks and more) with few rows: each band
+// re-reads the token operands of all of K, 4 KiB per 64 elements, for as
+// few as 16 rows, so the bands take four tiles and K is split to fill the
+// CUs (each wave keeping at least one super-block per split; the slabs are
+// summed in split order).  Measured at 3584 x 18944 (M = 4 / 16): 30.3 /
+// 30.8 us unsplit on 16-row bands, 27.1 / 28.0 us on 64-row bands in four
+// splits; at K = 4096 every split measured slower.
+int mmqs_plan(int N, int K, int cus, int* rows_per_wg) {
+    const int nsb = K / 256, mt = fq::mmqs_max_tiles();
+    const long bands4 = (N + 16 * mt - 1) / (16 * mt);
+    if (nsb >= 32 && 2 * bands4 <= cus) {
+        *rows_per_wg = 16 * mt;
+        const int s = (int)std::max(1L, std::min<long>(cus / bands4, nsb / 8));
+        const int sps = (nsb + s - 1) / s;
+        return (nsb + sps - 1) / sps;
+    }
+    *rows_per_wg = 16 * std::min(mt, std::max(1, (N + 16 * cus - 1) / (16 * cus)));
+    return 1;
+}
+
 // Workspace bytes and K-splits of the Q8_0 / Q4_0 prefill kernel (M > 32,
 // K a multiple of 256): one work-group per CU and tile, K split when that
 // shortens the busiest CU's work, each split a multiple of four 64-element
@@ -345,7 +367,10 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         const int NC = K / 64;
         const MmqPlan pl = plan_mmq(M, K, N, di.cus);
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-        const size_t need = 256 + al(pl.xop_b) + al(pl.xsum_b) + al(pl.ex_b);
+        int rpw = 0;
+        const int splits = mmqs_plan(N, K, di.cus, &rpw);
+        const size_t part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+        const size_t need = 256 + al(pl.xop_b) + al(pl.xsum_b) + al(pl.ex_b) + al(part_b);
         std::unique_ptr<StreamScratch::Lease> lease;
         uint8_t* buf = fixed;
         if (fixed) {
@@ -360,6 +385,9 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         a.xop = buf;
         a.xsum = reinterpret_cast<const float*>(buf + al(pl.xop_b));
         a.ex = reinterpret_cast<const int*>(buf + al(pl.xop_b) + al(pl.xsum_b));
+        a.part = splits > 1 ? reinterpret_cast<float*>(buf + al(pl.xop_b) + al(pl.xsum_b) +
+                                                       al(pl.ex_b))
+                            : nullptr;
         a.y = y;
         a.bias = bias;
         a.bias_len = bias_mode ? bias_len : 0;
@@ -372,9 +400,7 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         e = fq::launch_xprep((int)dtype, x, M, K, NC, reinterpret_cast<_Float16*>(buf),
                              const_cast<float*>(a.xsum), const_cast<int*>(a.ex), st);
         if (e != hipSuccess) return hip_fail(e);
-        const int rpw =
-            16 * std::min(fq::mmqs_max_tiles(), std::max(1, (N + 16 * di.cus - 1) / (16 * di.cus)));
-        e = fq::launch_mmqs((int)dtype, a, rpw, 512, st);
+        e = fq::launch_mmqs((int)dtype, a, rpw, 512, splits, st);
         return e == hipSuccess ? FQ_OK : hip_fail(e);
     }
 

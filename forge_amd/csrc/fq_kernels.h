@@ -110,7 +110,10 @@ hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, in
 // rows (at most 16 mmqs_max_tiles()) per work-group
 bool mmqs_supported(int dtype);
 int mmqs_max_tiles();
-hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hipStream_t st);
+// splits > 1: K split over blockIdx.y into a.part slabs (super-blocks
+// ceil(K/256 / splits) each), then launch_reduce adds them and the bias
+hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int splits,
+                       hipStream_t st);
 // prefill for Q8_0 / Q4_0 on v_mfma_f32_32x32x16_f16 (fq_mmqp.hip): token
 // operands of launch_xprep32 (a.xop, a.ex = one exponent per token), a.part
 // holds the split-K slabs when splits > 1 (then reduce with launch_reduce)

@@ -87,7 +87,7 @@ struct Band<Q4_K> {
 constexpr int NPL = 3;  // 16-byte pieces per lane per panel (144 / 64, rounded up)
 
 template <int F, int TW, int WG, bool BIAS>
-__global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
+__global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, int sb_per_split) {
     using B = Band<F>;
     constexpr int W = WG / 64;
     // per wave: TW panels (one super-block of 16 rows each) and TW tiles x 4
@@ -103,7 +103,10 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
     const int lo = blockIdx.x * rows_per_wg;
     const int hi = min(a.N, lo + rows_per_wg);
     const int ntl = (hi - lo + 15) >> 4;
-    const int nsb = a.K / B::SBK;
+    // this work-group's super-blocks: all of K, or split blockIdx.y of a K
+    // split whose partial sums go to slab blockIdx.y of a.part
+    const int sb0 = blockIdx.y * sb_per_split;
+    const int nsb = min(a.K / B::SBK, sb0 + sb_per_split);
 
     // piece p of a tile's panel (rows clamped into the matrix)
     const uint8_t* prow[TW];
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
     // chunks of the next super-block ahead of its panel loads, so that no
     // short L2 load queues behind a long HBM load in the in-order vector
     // memory counter, needs about 250 VGPRs and measured slower.)
-    int sb = wave;
+    int sb = sb0 + wave;
     fq_u32x4 pv[TW][NPL];
     fq_u32x4 xv[4];  // the token operands of the chunk computed next
     Xs xs{0, 0.0f, 0.0f};
@@ -234,6 +237,8 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) part[wave][t][4 * q + i][c] = acc[t][i];
     __syncthreads();
+    const bool split = gridDim.y > 1;
+    float* const out = split ? a.part + (size_t)blockIdx.y * a.M * a.N : a.y;
     for (int o = threadIdx.x; o < ntl * 256; o += WG) {
         const int t = o >> 8, rr = (o >> 4) & 15, m = o & 15;
         const int row = lo + 16 * t + rr;
@@ -241,10 +246,12 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg) {
         float v = part[0][t][rr][m];
         for (int w = 1; w < W; ++w) v += part[w][t][rr][m];
         if constexpr (BIAS) {
-            if (a.bias_mode == 2) v += a.bias[(size_t)m * a.N + row];
-            else v += row < a.bias_len ? a.bias[row] : 0.0f;
+            if (!split) {
+                if (a.bias_mode == 2) v += a.bias[(size_t)m * a.N + row];
+                else v += row < a.bias_len ? a.bias[row] : 0.0f;
+            }
         }
-        a.y[(size_t)m * a.N + row] = v;
+        out[(size_t)m * a.N + row] = v;
     }
 }
 
@@ -277,7 +284,8 @@ bool mmqs_supported(int dtype) { return dtype == Q4_K; }
 // rows).
 int mmqs_max_tiles() { return 4; }
 
-hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hipStream_t st) {
+hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int splits,
+                       hipStream_t st) {
     const int tw = (rows_per_wg + 15) / 16;
     const void* fn = nullptr;
     if (dtype == Q4_K) {
@@ -286,11 +294,17 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, hip
                           : sfn_tw<Q4_K, 512>(tw, a.bias_mode != 0);
     }
     if (!fn) return hipErrorInvalidValue;
+    const int nsb = a.K / 256;
+    if (splits < 1 || splits > nsb || (splits > 1 && !a.part)) return hipErrorInvalidValue;
+    int sps = (nsb + splits - 1) / splits;
+    splits = (nsb + sps - 1) / sps;  // no empty split
     const int grid = (a.N + rows_per_wg - 1) / rows_per_wg;
     MmqArgs args = a;
     int rpw = rows_per_wg;
-    void* params[] = {&args, &rpw};
-    return hipLaunchKernel(fn, dim3(grid), dim3(wg), params, 0, st);
+    void* params[] = {&args, &rpw, &sps};
+    const hipError_t e = hipLaunchKernel(fn, dim3(grid, splits), dim3(wg), params, 0, st);
+    if (e != hipSuccess || splits == 1) return e;
+    return launch_reduce(a, splits, st);
 }
 
 }  // namespace fq

@@ -127,3 +127,22 @@ def test_q4k_band_kernel(M, N, K):
     if M > 4:
         y4 = run(F.Q4_K, synth.make_weights(F.Q4_K, N, K, K + M), x[:4], N, K)
         assert np.array_equal(y[:4].view(np.uint32), y4.view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [4, 9, 16])
+@pytest.mark.parametrize("N,K", [(2000, 16384), (700, 18944)])
+def test_q4k_band_kernel_k_split(M, N, K):
+    # long rows on few rows: 64-row bands with K split over work-groups into
+    # partial slabs, summed in split order (8 and 9 splits here, the last
+    # split of 18944 shorter); both bias modes go through the slab sum
+    x = synth.make_x(M, K, seed=3 * N + M)
+    w = synth.make_weights(F.Q4_K, N, K, seed=K + 2 * M)
+    y = check(F.Q4_K, N, K, x, seed=K + 2 * M, what=f"q4_k split M={M} {N}x{K}")
+    assert np.array_equal(y.view(np.uint32), run(F.Q4_K, w, x, N, K).view(np.uint32))
+    b1 = synth.make_x(1, N, seed=5).reshape(N)
+    b2 = synth.make_x(M, N, seed=6)
+    y1 = run(F.Q4_K, w, x, N, K, bias=torch.from_numpy(b1).cuda())
+    y2 = run(F.Q4_K, w, x, N, K, bias=torch.from_numpy(b2).cuda())
+    tol = 1e-6 * float(np.max(np.abs(y)))
+    np.testing.assert_allclose(y1, y + b1[None, :], rtol=0, atol=tol)
+    np.testing.assert_allclose(y2, y + b2, rtol=0, atol=tol)
