@@ -236,7 +236,7 @@ struct Task<Q6_K> {
         for (int g = 0; g < 4; ++g) {  // elements l0 + 4g .. +4: 6-bit codes, then -32
             const uint32_t q6 = ((L[g] >> lsh) & 0x0F0F0F0Fu) | (((H[g] >> hsh) & 0x03030303u) << 4);
             h2 p0, p1;
-            byte_pairs(q6, 0x00FF00FFu, (_Float16)1056.0f, p0, p1);
+            byte_pairs(q6, (_Float16)1056.0f, p0, p1);
             *reinterpret_cast<h4*>(dst + (16 * g + c) * 4) = h4{p0[0], p0[1], p1[0], p1[1]};
         }
     }
@@ -378,7 +378,7 @@ struct Task<Q3_K> {
             const uint32_t q3 = ((Q[g] >> (2 * jp)) & 0x03030303u) |
                                 (((H[g] >> (4 * n + jp)) & 0x01010101u) << 2);
             h2 p0, p1;
-            byte_pairs(q3, 0x00FF00FFu, (_Float16)1028.0f, p0, p1);
+            byte_pairs(q3, (_Float16)1028.0f, p0, p1);
             *reinterpret_cast<h4*>(dst + (16 * g + c) * 4) = h4{p0[0], p0[1], p1[0], p1[1]};
         }
     }

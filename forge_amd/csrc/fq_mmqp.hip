@@ -140,18 +140,6 @@ __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ 
 }
 
 // -------------------------------------------------------- weight operands
-// Eight bytes as fp16 (value - off): v_perm pairs each byte with 0x64, so a
-// half reads 1024 + byte, in the slot order {0, 2, 1, 3} of each dword.
-__device__ __forceinline__ h8 perm8(uint32_t w0, uint32_t w1, _Float16 off) {
-    const h2 o = {off, off};
-    const uint32_t c = 0x64646464u;
-    const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c, w0, 0x04020400u)) - o;
-    const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c, w0, 0x04030401u)) - o;
-    const h2 d = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c, w1, 0x04020400u)) - o;
-    const h2 e = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c, w1, 0x04030401u)) - o;
-    return h8{a[0], a[1], b[0], b[1], d[0], d[1], e[0], e[1]};
-}
-
 template <int F>
 struct PB;
 
@@ -172,8 +160,8 @@ struct PB<Q8_0> {
     static constexpr bool MIN = false;          // no per-block minimum term
     template <int B>
     __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
-        b0 = perm8(q[0] ^ 0x80808080u, q[1] ^ 0x80808080u, (_Float16)1152.0f);
-        b1 = perm8(q[2] ^ 0x80808080u, q[3] ^ 0x80808080u, (_Float16)1152.0f);
+        b0 = byte8(q[0] ^ 0x80808080u, q[1] ^ 0x80808080u, (_Float16)1152.0f);
+        b1 = byte8(q[2] ^ 0x80808080u, q[3] ^ 0x80808080u, (_Float16)1152.0f);
     }
 };
 
@@ -219,8 +207,8 @@ struct PB<Q5_0> {
     static constexpr bool MIN = false;
     template <int B>
     __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
-        b0 = perm8(q[0], q[1], (_Float16)1040.0f);
-        b1 = perm8(q[2], q[3], (_Float16)1040.0f);
+        b0 = byte8(q[0], q[1], (_Float16)1040.0f);
+        b1 = byte8(q[2], q[3], (_Float16)1040.0f);
     }
 };
 template <>
@@ -230,8 +218,8 @@ struct PB<Q5_1> {
     static constexpr bool MIN = true;
     template <int B>
     __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
-        b0 = perm8(q[0], q[1], (_Float16)1024.0f);
-        b1 = perm8(q[2], q[3], (_Float16)1024.0f);
+        b0 = byte8(q[0], q[1], (_Float16)1024.0f);
+        b1 = byte8(q[2], q[3], (_Float16)1024.0f);
     }
 };
 
