@@ -197,10 +197,10 @@ int mmqs_plan(int N, int K, int cus, int* rows_per_wg) {
 // steps.
 struct MmqpPlan {
     int splits;
-    size_t xop_b, ex_b, sum_b, part_b, total;
+    size_t xop_b, ex_b, sum_b, part_b, q6c_b, total;
 };
 
-MmqpPlan plan_mmqp(int M, int K, int N, int cus) {
+MmqpPlan plan_mmqp(int M, int K, int N, int cus, bool q6k = false) {
     MmqpPlan p{};
     const int Tn = (M + 31) / 32, nsteps = K / 64;
     const int tn = fq::mmqp_tile_rows(), tm = fq::mmqp_tile_tokens();
@@ -226,8 +226,9 @@ MmqpPlan plan_mmqp(int M, int K, int N, int cus) {
     p.ex_b = (size_t)M * 4;
     p.sum_b = (size_t)Tn * 32 * K / 32 * 4;  // sub-block sums (formats with a min term)
     p.part_b = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
+    p.q6c_b = q6k ? (size_t)fq::mmqp_q6c_bytes(N, K) : 0;  // Q6_K rows as 36-byte blocks
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    p.total = 256 + al(p.xop_b) + al(p.ex_b) + al(p.sum_b) + al(p.part_b);
+    p.total = 256 + al(p.xop_b) + al(p.ex_b) + al(p.sum_b) + al(p.part_b) + al(p.q6c_b);
     return p;
 }
 
@@ -530,15 +531,17 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         }
     }
 
+    const bool q6k = dtype == FQ_DTYPE_Q6_K;
     if (fq::mmqp_supported((int)dtype) && M > 32 && K > 0 && K % 256 == 0 &&
-        (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
-        (int64_t)N * ((K / g.be) * g.bb) < ((int64_t)1 << 32)) {
-        // prefill, Q8_0 / Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q4_K rows that are whole 16-byte chunks (K
-        // a multiple of 256, 16-byte aligned weights, under 4 GiB of them:
-        // the copies take 32-bit offsets): per-token operands, then
-        // one work-group per CU and tile on v_mfma_f32_32x32x16_f16 (K-split
-        // while the tiles leave CUs idle)
-        const MmqpPlan pl = plan_mmqp(M, K, N, di.cus);
+        (q6k || (reinterpret_cast<uintptr_t>(w) & 15) == 0) &&
+        (int64_t)N * (q6k ? fq::mmqp_q6c_bytes(1, K) : (K / g.be) * g.bb) < ((int64_t)1 << 32)) {
+        // prefill, rows that are whole 16-byte chunks (K a multiple of 256,
+        // 16-byte aligned weights, under 4 GiB of them: the copies take
+        // 32-bit offsets): per-token operands, then one work-group per CU and
+        // tile on v_mfma_f32_32x32x16_f16 (K-split while the tiles leave CUs
+        // idle).  Q6_K rows are first rewritten into 36-byte blocks in the
+        // workspace
+        const MmqpPlan pl = plan_mmqp(M, K, N, di.cus, q6k);
         const int splits = pl.splits;
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
         const size_t xop_b = pl.xop_b, ex_b = pl.ex_b, sum_b = pl.sum_b, need = pl.total;
@@ -553,6 +556,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         }
         fq::MmqArgs a{};
         a.w = static_cast<const uint8_t*>(w);
+        a.row_bytes = (K / g.be) * g.bb;
+        if (q6k) {
+            uint8_t* conv = buf + al(xop_b) + al(ex_b) + al(sum_b) + al(pl.part_b);
+            e = fq::launch_q6c(static_cast<const uint8_t*>(w), N, K, a.row_bytes, conv, st);
+            if (e != hipSuccess) return hip_fail(e);
+            a.w = conv;
+            a.row_bytes = (int)fq::mmqp_q6c_bytes(1, K);
+        }
         a.xop = buf;
         a.ex = reinterpret_cast<const int*>(buf + al(xop_b));
         a.xsum = dtype == FQ_DTYPE_Q4_K || dtype == FQ_DTYPE_Q4_1 || dtype == FQ_DTYPE_Q5_1
@@ -567,9 +578,8 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         a.M = M;
         a.N = N;
         a.K = K;
-        a.row_bytes = (K / g.be) * g.bb;
         e = fq::launch_xprep32(x, M, K, reinterpret_cast<_Float16*>(buf),
-                               const_cast<int*>(a.ex), const_cast<float*>(a.xsum), st);
+                               const_cast<int*>(a.ex), const_cast<float*>(a.xsum), q6k, st);
         if (e != hipSuccess) return hip_fail(e);
         e = fq::launch_mmqp((int)dtype, a, splits, st);
         if (e == hipSuccess && splits > 1) e = fq::launch_reduce(a, splits, st);
@@ -1052,7 +1062,7 @@ int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
     for (int n = N_max; n > 0; n = n > 128 ? ((n - 1) / 128) * 128 : 0) {
         for (int m = 2; m <= M_max; ++m) {
             need0 = std::max(need0, plan_mmq(m, K_max, n, di.cus).total);
-            if (m > 32 && Kp > 0) need0 = std::max(need0, plan_mmqp(m, Kp, n, di.cus).total);
+            if (m > 32 && Kp > 0) need0 = std::max(need0, plan_mmqp(m, Kp, n, di.cus, true).total);
         }
     }
     const size_t need1 = 2 * (size_t)M_max * N_max * sizeof(float);

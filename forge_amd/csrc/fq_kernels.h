@@ -114,14 +114,21 @@ int mmqs_max_tiles();
 // ceil(K/256 / splits) each), then launch_reduce adds them and the bias
 hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int splits,
                        hipStream_t st);
-// prefill for Q8_0 / Q4_0 on v_mfma_f32_32x32x16_f16 (fq_mmqp.hip): token
+// prefill on v_mfma_f32_32x32x16_f16 (fq_mmqp.hip): token
 // operands of launch_xprep32 (a.xop, a.ex = one exponent per token), a.part
 // holds the split-K slabs when splits > 1 (then reduce with launch_reduce)
 bool mmqp_supported(int dtype);
 int mmqp_tile_rows();    // rows per work-group tile
 int mmqp_tile_tokens();  // tokens per work-group tile
+// sub16: the operand order of the Q6_K kernel (each 16-element quarter one
+// sub-block)
 hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, float* xsum,
-                          hipStream_t st);
+                          bool sub16, hipStream_t st);
+// Q6_K: the kernel reads 36-byte blocks that launch_q6c writes from the GGUF
+// rows (mmqp_q6c_bytes(N, K) bytes, 16-byte aligned)
+int64_t mmqp_q6c_bytes(int N, int K);
+hipError_t launch_q6c(const uint8_t* w, int N, int K, int64_t row_bytes, uint8_t* out,
+                      hipStream_t st);
 hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st);
 hipError_t launch_reduce(const MmqArgs& a, int splits, hipStream_t st);
 hipError_t launch_dequant(int dtype, const uint8_t* w, float* out, int N, int K, int U,

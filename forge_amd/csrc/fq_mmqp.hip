@@ -1,5 +1,5 @@
-// fq_mmqp.hip -- prefill (M > 32 tokens) for Q8_0, Q4_0, Q4_1 and Q4_K on
-// v_mfma_f32_32x32x16_f16.
+// fq_mmqp.hip -- prefill (M > 32 tokens) for Q8_0, Q4_0, Q4_1, Q5_0, Q5_1,
+// Q4_K and Q6_K on v_mfma_f32_32x32x16_f16.
 //
 //   D[token][n] = X[token][k] . W[n][k]^T on the fp16 matrix cores, with the
 // tokens as x 2^-e(token) in fp16 hi + lo and the weights' integer codes
@@ -9,7 +9,9 @@
 //
 // Token prep is one launch (xprep4_kernel): the per-token exponent, then the
 // hi/lo operands in the A-operand layout (and the per-token block sums for
-// the minimum term).
+// the minimum term).  Q6_K, whose scales cover 16 elements, first goes
+// through q6c_kernel into 36-byte blocks of int8 codes (below) and uses the
+// operand order in which each MFMA covers one 16-element sub-block.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,7 +40,9 @@ constexpr int NW = 8;                // waves per work-group
 // hi + lo, written as the A operand of v_mfma_f32_32x32x16_f16: for token
 // tile T = m / 32 and quarter kq (the MFMA half kq % 2 of block kq / 2), lane
 // (m % 32) + 32 g holds elements 32 (kq / 2) + 16 g + 8 (kq % 2) +
-// slot_elem(j), j = 0..7, the hi block then the lo block 512 halves on.
+// slot_elem(j), j = 0..7, the hi block then the lo block 512 halves on
+// (SUB16: elements 16 kq + 8 g + slot_elem(j), so that each quarter is one
+// 16-element sub-block).
 //
 // One launch: work-group j owns tokens 4 j .. 4 j + 3 (all of K).  Piece p = ((2 kq + g) 4 + t): token t's eight elements of quarter kq,
 // lane group g -- four consecutive threads write one 64-byte run (hi, and
@@ -46,6 +50,7 @@ constexpr int NW = 8;                // waves per work-group
 // HBM), pass 2 writes the operands from the values kept in registers (those
 // of K beyond 8192 are read again, from L2).  The work-groups cover every
 // token slot of the last tile (slots past M are zero).
+template <bool SUB16>
 __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ x, int M, int K,
                                                       int* __restrict__ ex,
                                                       _Float16* __restrict__ xop,
@@ -59,7 +64,7 @@ __global__ __launch_bounds__(1024) void xprep4_kernel(const float* __restrict__ 
     const int KQ = K / 16, P = 8 * KQ;  // pieces per work-group
     auto src = [&](int p) {
         const int gq = p >> 2, g = gq & 1, kq = gq >> 1;
-        return xr + 32 * (kq >> 1) + 16 * g + 8 * (kq & 1);
+        return SUB16 ? xr + 16 * kq + 8 * g : xr + 32 * (kq >> 1) + 16 * g + 8 * (kq & 1);
     };
     // the first CP pieces of a thread stay in registers for the second pass
     // (all of them up to K = 8192); the rest are read again, from L2
@@ -243,6 +248,25 @@ struct PB<Q4_K> {
     }
 };
 
+// Q6_K as converted by q6c_kernel (36-byte blocks of 32 elements): d @0,
+// the two sub-block scales int8 @2, @3, then the 32 codes q - 32 as int8
+// @4, stored so that lane group g's 16 bytes are elements 8 g .. 8 g + 7 of
+// sub-block 0 then of sub-block 1: half h of the MFMA is sub-block h, in the
+// SUB16 operand order of xprep4_kernel.  Codes as Q8_0 (+128 via the sign
+// bit, then -1152).
+template <>
+struct PB<Q6_K> {
+    static constexpr int BB = 36, SB = 2 * BB;
+    static constexpr int GS = 16;
+    static constexpr int QOFF = 4;
+    static constexpr bool MIN = false;
+    template <int B>
+    __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
+        b0 = byte8(q[0] ^ 0x80808080u, q[1] ^ 0x80808080u, (_Float16)1152.0f);
+        b1 = byte8(q[2] ^ 0x80808080u, q[3] ^ 0x80808080u, (_Float16)1152.0f);
+    }
+};
+
 // Chunks per row and step, and the byte offset (within the row) of chunk p
 // of step s, less 16 p.  Q8_0 / Q4_0: a step of a row (68 / 36 bytes)
 // starts (s SB) mod 16 = 0, 4, 8 or 12 bytes into a 16-byte chunk (rows are
@@ -254,6 +278,12 @@ struct Chunks {
     // multiple of 4 and rows 16-byte aligned)
     static constexpr int o4(int u) { return u * PB<F>::SB & 15; }
     __device__ static size_t off(int s, int) { return (size_t)s * PB<F>::SB & ~(size_t)15; }
+};
+template <>
+struct Chunks<Q6_K> {  // a step (72 bytes) starts 0 or 8 bytes into a chunk
+    static constexpr int CH = 5;
+    static constexpr int o4(int u) { return u * 72 & 15; }
+    __device__ static size_t off(int s, int) { return (size_t)s * 72 & ~(size_t)15; }
 };
 template <>
 struct Chunks<Q5_1> {  // a step (48 bytes) starts on a chunk
@@ -335,6 +365,12 @@ __device__ __forceinline__ void scales(const uint8_t* row, float& db, float& mn)
         Fmt<Q4_K>::scale_min(uint4{h[0], h[1], h[2], h[3]}, O4 / 4, sa, ma, sb, mb);
         db = f16_hw(h[0] & 0xFFFFu) * (float)(B ? sb : sa);
         mn = f16_hw(h[0] >> 16) * (float)(B ? mb : ma);
+    } else if constexpr (F == Q6_K) {  // db = d sc1 and mn = sc0 / sc1 (sc1 = 0: d sc0, 1)
+        const uint32_t h = lds4_a2(row + O4 + PB<F>::BB * B);
+        const float d = f16_hw(h & 0xFFFFu);
+        const float s0 = (float)(int8_t)(h >> 16), s1 = (float)(int8_t)(h >> 24);
+        db = d * (s1 != 0.0f ? s1 : s0);
+        mn = s1 != 0.0f ? s0 / s1 : 1.0f;
     } else if constexpr (F == Q4_1 || F == Q5_1) {
         const uint32_t dm = lds4_a2(row + O4 + PB<F>::BB * B);
         db = f16_hw(dm & 0xFFFFu);
@@ -506,39 +542,84 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
                     P::template ops<1>(q, g, B[j][0], B[j][1]);
                     scales<F, O4, 1>(row, db[j], mn[j][1]);
                 }
+                if constexpr (F == Q6_K) {
+                    // sc1 = 0: the second sub-block's weights are zero
+                    const h8 zero = {};
+                    if (mn[j][b] == 1.0f && *(row + O4 + PB<F>::BB * b + 3) == 0) B[j][1] = zero;
+                }
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int st = 2 * b + i;  // stage within the step
                 h8(&cur)[4] = A[st & 1];
                 if (st < 3) read_a(xs, (st + 1) >> 1, (st + 1) & 1, A[(st + 1) & 1]);
-                f32x16 d[2];
-                const f32x16 z = {};
+                if constexpr (F == Q6_K) {
+                    // one chain over both 16-element sub-blocks: the first
+                    // sub-block's partial sums are scaled by r = sc0 / sc1
+                    // before the second's MFMAs add to them, and the block
+                    // folds with d sc1 (scales(): db = d sc1, mn = r); a zero
+                    // sc1 zeroes the second sub-block's codes instead (r = 1,
+                    // db = d sc0)
+                    f32x16 d[2];
+                    const f32x16 z = {};
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[0], B[j][0], z, 0, 0, 0);
+                    for (int j = 0; j < 2; ++j)
+                        d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[0], B[j][0], z, 0, 0, 0);
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[1], B[j][0], d[j], 0, 0, 0);
+                    for (int j = 0; j < 2; ++j)
+                        d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[1], B[j][0], d[j], 0, 0, 0);
+                    // the previous stage's fold covers these MFMAs' latency
+                    if (pend) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[2], B[j][1], d[j], 0, 0, 0);
+                        for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[3], B[j][1], d[j], 0, 0, 0);
-                // fold the previous stage (token tile 1 - i)
-                if (pend) {
+                            for (int e = 0; e < 16; ++e)
+                                acc[1 - i][j][e] = __builtin_fmaf(dbp[j], dp[j][e], acc[1 - i][j][e]);
+                    }
 #pragma unroll
                     for (int j = 0; j < 2; ++j)
 #pragma unroll
-                        for (int e = 0; e < 16; ++e)
-                            acc[1 - i][j][e] = __builtin_fmaf(dbp[j], dp[j][e], acc[1 - i][j][e]);
+                        for (int e = 0; e < 16; ++e) d[j][e] *= mn[j][b];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[2], B[j][1], d[j], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[3], B[j][1], d[j], 0, 0, 0);
+                    dp[0] = d[0];
+                    dp[1] = d[1];
+                    dbp[0] = db[0];
+                    dbp[1] = db[1];
+                    pend = true;
+                } else {
+                    f32x16 d[2];
+                    const f32x16 z = {};
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[0], B[j][0], z, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[1], B[j][0], d[j], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[2], B[j][1], d[j], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        d[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[3], B[j][1], d[j], 0, 0, 0);
+                    // fold the previous stage (token tile 1 - i)
+                    if (pend) {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+#pragma unroll
+                            for (int e = 0; e < 16; ++e)
+                                acc[1 - i][j][e] = __builtin_fmaf(dbp[j], dp[j][e], acc[1 - i][j][e]);
+                    }
+                    dp[0] = d[0];
+                    dp[1] = d[1];
+                    dbp[0] = db[0];
+                    dbp[1] = db[1];
+                    pend = true;
                 }
-                dp[0] = d[0];
-                dp[1] = d[1];
-                dbp[0] = db[0];
-                dbp[1] = db[1];
-                pend = true;
             }
         }
         if constexpr (TL::MIN) {
@@ -613,20 +694,88 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
     }
 }
 
+// ------------------------------------------------------ Q6_K conversion
+// GGUF Q6_K rows (210-byte super-blocks, matmul.cpp:242-279: element
+// 128 h + 32 k + l of a super-block is nibble k / 2 of ql[64 h + 32 (k % 2)
+// + l] with bits 2 k, 2 k + 1 of qh[32 h + l] on top, minus 32, scale
+// sc[8 h + 2 k + l / 16]) -> 36-byte blocks of 32 elements (PB<Q6_K>): d,
+// the block's two sub-block scales, the 32 codes as int8, bytes 8 g .. 8 g +
+// 7 of each 16 holding elements 8 g .. of sub-block 0 then of sub-block 1.
+// One thread per block; its 32 ql and 32 qh bytes are read as 16-byte loads
+// from their 2-byte-aligned addresses (gfx950 serves unaligned loads).
+__global__ __launch_bounds__(256) void q6c_kernel(const uint8_t* __restrict__ w, int N, int K,
+                                                  int64_t row_bytes, uint8_t* __restrict__ out) {
+    const int nb = K / 32;
+    const size_t total = (size_t)N * nb;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * 256) {
+        const int n = (int)(i / nb), bi = (int)(i - (size_t)n * nb);
+        const int sbi = bi >> 3, h = (bi >> 2) & 1, k = bi & 3;
+        const uint8_t* sb = w + (size_t)n * row_bytes + (size_t)210 * sbi;
+        const uint4* qlp = reinterpret_cast<const uint4*>(sb + 64 * h + 32 * (k & 1));
+        const uint4* qhp = reinterpret_cast<const uint4*>(sb + 128 + 32 * h);
+        const uint4 l0 = qlp[0], l1 = qlp[1], h0 = qhp[0], h1 = qhp[1];
+        const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+        const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        const uint16_t sc = *reinterpret_cast<const uint16_t*>(sb + 192 + 8 * h + 2 * k);
+        const uint16_t d = *reinterpret_cast<const uint16_t*>(sb + 208);
+        uint8_t c[32];  // codes in element order, + 128 offset removed below
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t nib = ((lw[u] >> (8 * v)) >> (4 * (k >> 1))) & 0xFu;
+                const uint32_t hb = ((hw[u] >> (8 * v)) >> (2 * k)) & 0x3u;
+                c[4 * u + v] = (uint8_t)((int)(nib | (hb << 4)) - 32);
+            }
+        }
+        uint32_t o[9];
+        o[0] = (uint32_t)d | ((uint32_t)sc << 16);
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {  // dword p: bytes 4 p .. 4 p + 3 of the code area
+            uint32_t v = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int q = 4 * p + b;  // byte q holds element e (layout above)
+                const int e = (q & 7) + 8 * ((q >> 4) & 1) + 16 * ((q >> 3) & 1);
+                v |= (uint32_t)c[e] << (8 * b);
+            }
+            o[1 + p] = v;
+        }
+        uint32_t* dst = reinterpret_cast<uint32_t*>(out + i * 36);
+#pragma unroll
+        for (int p = 0; p < 9; ++p) dst[p] = o[p];
+    }
+}
+
 }  // namespace
 
 bool mmqp_supported(int dtype) {
     return dtype == Q8_0 || dtype == Q4_0 || dtype == Q4_1 || dtype == Q5_0 || dtype == Q5_1 ||
-           dtype == Q4_K;
+           dtype == Q4_K || dtype == Q6_K;
+}
+
+int64_t mmqp_q6c_bytes(int N, int K) { return (int64_t)N * (K / 32) * 36; }
+
+hipError_t launch_q6c(const uint8_t* w, int N, int K, int64_t row_bytes, uint8_t* out,
+                      hipStream_t st) {
+    const size_t total = (size_t)N * (K / 32);
+    const int grid = (int)std::min<size_t>((total + 255) / 256, 16384);
+    hipLaunchKernelGGL(q6c_kernel, dim3(grid), dim3(256), 0, st, w, N, K, row_bytes, out);
+    return hipGetLastError();
 }
 int mmqp_tile_rows() { return BNT; }
 int mmqp_tile_tokens() { return BMT; }
 
 hipError_t launch_xprep32(const float* x, int M, int K, _Float16* xop, int* ex, float* xsum,
-                          hipStream_t st) {
+                          bool sub16, hipStream_t st) {
     if (K % 256 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(xprep4_kernel, dim3(8 * ((M + 31) / 32)), dim3(1024), 0, st, x, M, K, ex,
-                       xop, xsum);
+    if (sub16)
+        hipLaunchKernelGGL(xprep4_kernel<true>, dim3(8 * ((M + 31) / 32)), dim3(1024), 0, st, x, M,
+                           K, ex, xop, xsum);
+    else
+        hipLaunchKernelGGL(xprep4_kernel<false>, dim3(8 * ((M + 31) / 32)), dim3(1024), 0, st, x,
+                           M, K, ex, xop, xsum);
     return hipGetLastError();
 }
 
@@ -647,6 +796,8 @@ hipError_t launch_mmqp(int dtype, const MmqArgs& a, int splits, hipStream_t st) 
         hipLaunchKernelGGL(mmqp_kernel<Q5_1>, grid, dim3(64 * NW), 0, st, a, sps);
     else if (dtype == Q4_K)
         hipLaunchKernelGGL(mmqp_kernel<Q4_K>, grid, dim3(64 * NW), 0, st, a, sps);
+    else if (dtype == Q6_K)
+        hipLaunchKernelGGL(mmqp_kernel<Q6_K>, grid, dim3(64 * NW), 0, st, a, sps);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -27,7 +27,8 @@
  *    1163-1165, 1315) or launches unchecked.
  *  - Calls on the M > 1 matrix-core path and the GGUF fused ops use a
  *    library-owned per-device, per-stream workspace (token operands, split-K
- *    partial slabs, intermediate rows).  It grows on demand inside a call
+ *    partial slabs, intermediate rows; for Q6_K prefill, M > 32, the rows
+ *    rewritten into 36-byte blocks of int8 codes: N * K * 9 / 8 bytes).  It grows on demand inside a call
  *    (hipMalloc, no host synchronisation; a superseded buffer is kept until
  *    fq_release_workspace) and lives until the process ends.  Under HIP-graph
  *    capture a call that would have to grow it returns FQ_ERR_WORKSPACE:
@@ -213,7 +214,8 @@ int fq_ffn_down_residual_packed(uint32_t dtype, const float* x, const void* w_pa
  * reference: it is for callers that cannot allocate (code under HIP-graph
  * capture, serving loops and harnesses that forbid hipMalloc).  Returns
  * FQ_ERR_WORKSPACE when a call needs more than 64 MiB (for example M = 512 at
- * K = N = 4096 needs 40-42 MiB with 4 K-splits).  All calls on one GPU
+ * K = N = 4096 needs 40-42 MiB with 4 K-splits, 58 MiB for Q6_K, whose
+ * rewritten rows take N * K * 9 / 8 bytes more).  All calls on one GPU
  * share the array: calls that overlap on one GPU (several streams or host
  * threads) race on it and must be serialised by the caller. */
 int fq_matmul_transB_noalloc(uint32_t dtype, const float* x, const void* w, const float* bias,
@@ -222,7 +224,8 @@ int fq_matmul_transB_noalloc(uint32_t dtype, const float* x, const void* w, cons
 
 /* Sizes the calling stream's workspace (current device) for every call with
  * at most M_max tokens, K_max columns and N_max rows, so that later calls
- * allocate nothing and can be captured into a HIP graph.  Replaces the
+ * allocate nothing and can be captured into a HIP graph.  The size covers
+ * every format, Q6_K prefill's rewritten rows included.  Replaces the
  * reference's grow-on-first-use scratch (src/operators/cpu/matmul.cpp:31-54,
  * the thread-local buffer behind the CUDA Q8_0 M > 32 path), which has no
  * reserve call of its own. */

@@ -2,7 +2,8 @@
 of 256, else fq_mmq.hip) against the oracle.
 
 Edge cases beyond the token-count and format sweeps of test_gpu_mmq.py, for
-the two prefill formats of the benchmark (Q8_0, Q4_0), Q4_1 and Q4_K: N and M tails with
+the two prefill formats of the benchmark (Q8_0, Q4_0), Q4_1, Q4_K, Q5_0, Q5_1
+and Q6_K (rewritten into 36-byte blocks before the kernel): N and M tails with
 one row and one block of K, block scales up to the fp16 maximum (and fp16
 subnormal ones in the same row), activations spanning 60 decades inside one
 token, bias modes, determinism, and an activation pointer that is only
@@ -22,7 +23,7 @@ from test_gpu_parity import dev_weight, run
 
 pytestmark = pytest.mark.gpu
 
-PREFILL = [F.Q8_0, F.Q4_0, F.Q4_1, F.Q4_K, F.Q5_0, F.Q5_1]
+PREFILL = [F.Q8_0, F.Q4_0, F.Q4_1, F.Q4_K, F.Q5_0, F.Q5_1, F.Q6_K]
 
 
 def check(dtype, w, x, N, K, what, bias=None):
@@ -66,14 +67,15 @@ def test_large_block_scales(dtype):
     f = F.fmt(dtype)
     nb = K // f.block_elems
     w = synth.make_weights(dtype, N, K, seed=21).reshape(N, nb, f.block_bytes)
+    d0 = 208 if dtype == F.Q6_K else 0  # the block's fp16 d
     rng = np.random.default_rng(22)
     big = np.array([300.0, 4000.0, 65504.0, -20000.0], np.float16)
     for r in (0, 5, 130, 255):
         cols = rng.choice(nb, size=min(8, nb), replace=False)
-        w[r, cols, 0:2] = rng.choice(big, size=len(cols)).view(np.uint8).reshape(len(cols), 2)
-    w[77, :, 0:2] = np.array([1e-7], np.float16).view(np.uint8)  # subnormal
-    w[77, 3, 0:2] = np.array([65504.0], np.float16).view(np.uint8)
-    w[200, :, 0:2] = np.array([1000.0], np.float16).view(np.uint8)  # a whole row
+        w[r, cols, d0:d0 + 2] = rng.choice(big, size=len(cols)).view(np.uint8).reshape(len(cols), 2)
+    w[77, :, d0:d0 + 2] = np.array([1e-7], np.float16).view(np.uint8)  # subnormal
+    w[77, 3, d0:d0 + 2] = np.array([65504.0], np.float16).view(np.uint8)
+    w[200, :, d0:d0 + 2] = np.array([1000.0], np.float16).view(np.uint8)  # a whole row
     w = w.reshape(N, -1)
     x = synth.make_x(M, K, seed=23)
     check(dtype, w, x, N, K, f"{F.fmt(dtype).name} large scales")
@@ -122,3 +124,33 @@ def test_unaligned_activations(dtype):
     y64 = oracle.matmul_f64(dtype, x_np, w_np, N, K)
     deq_max = float(np.max(np.abs(oracle.dequant(dtype, w_np, N, K))))
     assert_close(y, y64, x_np, np.array([deq_max]), "unaligned x")
+
+
+@pytest.mark.parametrize("offset", [0, 2])
+def test_q6k_sub_block_scales(offset):
+    # Q6_K: each 32-element block carries two 16-element sub-block scales,
+    # the first folded into the chain as sc0 / sc1; zero, extreme and
+    # sign-flipped pairs, whole rows of zero scales, and a weight pointer
+    # that is only 2-byte aligned (the rewrite reads the GGUF bytes in place)
+    M, N, K = 96, 300, 2048
+    nsb = K // 256
+    w = synth.make_weights(F.Q6_K, N, K, seed=31).reshape(N, nsb, 210)
+    rng = np.random.default_rng(32)
+    sc = w[:, :, 192:208].view(np.int8)
+    pairs = np.array([[0, 5], [5, 0], [0, 0], [-128, 127], [127, -128], [-128, -128],
+                      [1, -1], [64, 64]], np.int8)
+    for r in range(0, N, 3):
+        for s in range(nsb):
+            k = rng.integers(0, 8, size=4)
+            sc[r, s, 0:8] = pairs[k].reshape(-1)
+    sc[10] = 0                   # every scale of a row zero
+    sc[11, :, 1::2] = 0          # every second sub-block zero
+    w = w.reshape(N, -1)
+    x = synth.make_x(M, K, seed=33)
+    w_dev = dev_weight(F.Q6_K, w, N, K, offset)
+    xt = torch.from_numpy(x).cuda()
+    y = ops.matmul_transB(xt, w_dev).cpu().numpy()
+    y64 = oracle.matmul_f64(F.Q6_K, x, w, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(F.Q6_K, w, N, K))))
+    assert_close(y, y64, x, np.array([deq_max]), f"q6_k scales offset={offset}")
+    assert np.all(y[:, 10] == 0.0)

@@ -57,6 +57,7 @@ def test_noalloc_every_m_path():
 def test_noalloc_prefill_and_limit():
     _pair(F.Q8_0, 512, 4096, 4096, 60)  # 42 MiB of the 64 MiB: 4 K-splits
     _pair(F.Q4_0, 64, 1024, 512, 61)
+    _pair(F.Q6_K, 128, 2048, 1024, 62)  # the rows rewritten into the fixed array too
     L = _lib.lib()
     M, K, N = 1024, 16384, 256  # token operands alone need 272 MiB
     w = torch.zeros(N * (K // 32) * 34, dtype=torch.uint8, device="cuda")
