@@ -71,11 +71,14 @@ def test_growth_under_capture_is_refused():
 
 
 @pytest.mark.parametrize("dtype,M,K,N", [(F.Q8_0, 40, 4096, 256), (F.Q4_0, 512, 1280, 4096),
-                                         (F.Q4_K, 16, 4096, 2000), (F.Q8_0, 8, 2048, 3000)])
+                                         (F.Q4_K, 16, 4096, 2000), (F.Q8_0, 8, 2048, 3000),
+                                         (F.Q6_K, 96, 2048, 1500)])
 def test_reserve_then_capture_first(dtype, M, K, N):
     # fq_reserve_workspace alone (no eager call first) must cover the call's
-    # kernel choice: the prefill kernel (Q8_0 / Q4_0, up to 16 K-splits), the
-    # MMQ and small-batch paths
+    # kernel choice: the prefill kernel (Q8_0 / Q4_0, up to 16 K-splits; Q6_K
+    # with its rewritten rows), the MMQ and small-batch paths.  Three
+    # replays, each checked against the eager call, with eager work between
+    # them
     L = _lib.lib()
     w = torch.from_numpy(synth.make_weights(dtype, N, K, 41).reshape(-1)).cuda()
     x = torch.from_numpy(synth.make_x(M, K, 42)).cuda()
@@ -89,11 +92,18 @@ def test_reserve_then_capture_first(dtype, M, K, N):
     with torch.cuda.graph(g, stream=side):
         st = _mm(L, dtype, x, w, y_graph, M, K, N, side.cuda_stream)
     assert st == 0, L.fq_status_str(st)
-    g.replay()
-    torch.cuda.synchronize()
     with torch.cuda.stream(side):
         assert _mm(L, dtype, x, w, y_eager, M, K, N, side.cuda_stream) == 0
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(y_graph.cpu().numpy(), y_eager.cpu().numpy())
+    ref = y_eager.cpu().numpy()
+    for _ in range(3):
+        y_graph.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y_graph.cpu().numpy(), ref)
+        with torch.cuda.stream(side):
+            assert _mm(L, dtype, x, w, y_eager, M, K, N, side.cuda_stream) == 0
+        torch.cuda.synchronize()
     del g
     assert L.fq_release_workspace(side.cuda_stream) == 0
