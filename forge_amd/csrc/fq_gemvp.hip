@@ -538,9 +538,15 @@ constexpr int WGP = 1024;
 // Steps of weight loads a wave keeps in flight.  One, with 16 waves per CU,
 // measured fastest at every packed shape (cfg2 gate 10.3 us against 10.7 with
 // two and 12.3 with three).  GGUF rows of matrices of 64k rows and more
-// (lm_head) keep three: 81.4 us against 86.3 with one.
+// (lm_head) keep more: 81.4 us against 86.3 with one for Q6_K.  At
+// 152064 x 3584 (us, two / three / four steps): Q6_K 75.3 / 76.2 / 82.3,
+// Q8_0 91.3 / 92.8 / 94.3, Q4_0 67.1 / 65.4 / 65.3.
 constexpr int DP = 1;
-constexpr int DPG_DEEP = 3;
+template <int F>
+constexpr int deep_depth() {
+    return F == Q4_0 || F == Q4_1 ? 3 : 2;
+}
+constexpr int DPG_DEEP = 3;  // the deepest of deep_depth<F>() (launch geometry)
 constexpr int DEEP_ROWS = 65536;
 
 // Two lane units per lane hold both units' activation limbs in registers:
@@ -603,7 +609,7 @@ const void* gfn2(bool bias, bool deep) {
     if constexpr (GP > max_pieces<F>() * NL) {
         return nullptr;
     } else {
-        return deep ? gfn3<F, NL, GP, DPG_DEEP>(bias) : gfn3<F, NL, GP, depth<NL>()>(bias);
+        return deep ? gfn3<F, NL, GP, deep_depth<F>()>(bias) : gfn3<F, NL, GP, depth<NL>()>(bias);
     }
 }
 
