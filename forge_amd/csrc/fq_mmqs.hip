@@ -150,10 +150,10 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
                   a.xsum[(size_t)ch * XSUM + 16 + c]};
     };
 
-    // Token operands are prefetched one chunk ahead.  (Loading all four
-    // chunks of the next super-block ahead of its panel loads, so that no
-    // short L2 load queues behind a long HBM load in the in-order vector
-    // memory counter, needs about 250 VGPRs and measured slower.)
+    // Token operands are prefetched one chunk ahead, the next super-block's
+    // panels two chunks ahead (below).  (Loading all four chunks of the next
+    // super-block ahead of its panel loads needs about 250 VGPRs and
+    // measured slower.)
     int sb = sb0 + wave;
     fq_u32x4 pv[TW][NPL];
     fq_u32x4 xv[4];  // the token operands of the chunk computed next
@@ -171,18 +171,19 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
                 if (lane + 64 * i < B::PIECES)
                     *reinterpret_cast<fq_u32x4*>(&panels[wave][t][16 * (lane + 64 * i)]) = pv[t][i];
         const int nx = sb + W;
-        load_panels(min(nx, nsb - 1), pv);  // the next super-block's loads (clamped)
         // the super-block's coefficients: lane (r, q) decodes pair q of row r
         // (the wave's own LDS writes precede its reads: in order)
+        // (every tile of the band, also those past its last row: their
+        // panels repeat the matrix's last row and their sums are never
+        // written, and a branch per tile would keep the tiles' LDS reads,
+        // MFMAs and FMAs from overlapping)
 #pragma unroll
         for (int t = 0; t < TW; ++t) {
-            if (t < ntl) {
-                const float4 cv = B::coef4(panels[wave][t], q, r);
-                coef[wave][t][q][0][r] = cv.x;
-                coef[wave][t][q][1][r] = cv.y;
-                coef[wave][t][q][2][r] = cv.z;
-                coef[wave][t][q][3][r] = cv.w;
-            }
+            const float4 cv = B::coef4(panels[wave][t], q, r);
+            coef[wave][t][q][0][r] = cv.x;
+            coef[wave][t][q][1][r] = cv.y;
+            coef[wave][t][q][2][r] = cv.z;
+            coef[wave][t][q][3][r] = cv.w;
         }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -193,36 +194,39 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
             const int cn = g < 3 ? ch + 1 : 4 * min(nx, nsb - 1);
             load_x(cn, xn);
             const Xs xsn = load_s(cn);
+            // the next super-block's weight panels (clamped), two chunks
+            // ahead of their use and behind the last token loads this
+            // super-block waits for, so that no chunk's token operands queue
+            // behind them in the in-order vector memory counter
+            if (g == 2) load_panels(min(nx, nsb - 1), pv);
             const float S0 = xs.S0, S1 = xs.S1;
             const float p2 = __builtin_amdgcn_ldexpf(1.0f, xs.e);
             const h8 xh0 = __builtin_bit_cast(h8, xv[0]), xl0 = __builtin_bit_cast(h8, xv[1]);
             const h8 xh1 = __builtin_bit_cast(h8, xv[2]), xl1 = __builtin_bit_cast(h8, xv[3]);
 #pragma unroll
             for (int t = 0; t < TW; ++t) {
-                if (t < ntl) {  // wave-uniform
-                    h8 a0, a1;
-                    B::operands(panels[wave][t], g, r, q, a0, a1);
-                    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xh0, z, 0, 0, 0);
-                    d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xl0, d0, 0, 0, 0);
-                    f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xh1, z, 0, 0, 0);
-                    d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xl1, d1, 0, 0, 0);
-                    const float4 A0 = *reinterpret_cast<const float4*>(&coef[wave][t][g][0][4 * q]);
-                    const float4 A1 = *reinterpret_cast<const float4*>(&coef[wave][t][g][1][4 * q]);
-                    const float4 B0 = *reinterpret_cast<const float4*>(&coef[wave][t][g][2][4 * q]);
-                    const float4 B1 = *reinterpret_cast<const float4*>(&coef[wave][t][g][3][4 * q]);
-                    const float a0v[4] = {A0.x, A0.y, A0.z, A0.w};
-                    const float a1v[4] = {A1.x, A1.y, A1.z, A1.w};
-                    const float b0v[4] = {B0.x, B0.y, B0.z, B0.w};
-                    const float b1v[4] = {B1.x, B1.y, B1.z, B1.w};
+                h8 a0, a1;
+                B::operands(panels[wave][t], g, r, q, a0, a1);
+                const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xh0, z, 0, 0, 0);
+                d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, xl0, d0, 0, 0, 0);
+                f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xh1, z, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, xl1, d1, 0, 0, 0);
+                const float4 A0 = *reinterpret_cast<const float4*>(&coef[wave][t][g][0][4 * q]);
+                const float4 A1 = *reinterpret_cast<const float4*>(&coef[wave][t][g][1][4 * q]);
+                const float4 B0 = *reinterpret_cast<const float4*>(&coef[wave][t][g][2][4 * q]);
+                const float4 B1 = *reinterpret_cast<const float4*>(&coef[wave][t][g][3][4 * q]);
+                const float a0v[4] = {A0.x, A0.y, A0.z, A0.w};
+                const float a1v[4] = {A1.x, A1.y, A1.z, A1.w};
+                const float b0v[4] = {B0.x, B0.y, B0.z, B0.w};
+                const float b1v[4] = {B1.x, B1.y, B1.z, B1.w};
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float s = a0v[i] * d0[i];
-                        s = __builtin_fmaf(a1v[i], d1[i], s);
-                        s = __builtin_fmaf(b0v[i], S0, s);
-                        s = __builtin_fmaf(b1v[i], S1, s);
-                        acc[t][i] = __builtin_fmaf(s, p2, acc[t][i]);
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    float s = a0v[i] * d0[i];
+                    s = __builtin_fmaf(a1v[i], d1[i], s);
+                    s = __builtin_fmaf(b0v[i], S0, s);
+                    s = __builtin_fmaf(b1v[i], S1, s);
+                    acc[t][i] = __builtin_fmaf(s, p2, acc[t][i]);
                 }
             }
 #pragma unroll
