@@ -249,11 +249,11 @@ struct PB<Q4_K> {
 };
 
 // Q6_K as converted by q6c_kernel (36-byte blocks of 32 elements): d @0,
-// the two sub-block scales int8 @2, @3, then the 32 codes q - 32 as int8
+// the two sub-block scales int8 @2, @3, then the 32 six-bit codes q (0..63)
 // @4, stored so that lane group g's 16 bytes are elements 8 g .. 8 g + 7 of
 // sub-block 0 then of sub-block 1: half h of the MFMA is sub-block h, in the
-// SUB16 operand order of xprep4_kernel.  Codes as Q8_0 (+128 via the sign
-// bit, then -1152).
+// SUB16 operand order of xprep4_kernel.  A code becomes fp16 1024 + q, then
+// q - 32 after subtracting 1056.
 template <>
 struct PB<Q6_K> {
     static constexpr int BB = 36, SB = 2 * BB;
@@ -262,8 +262,8 @@ struct PB<Q6_K> {
     static constexpr bool MIN = false;
     template <int B>
     __device__ static void ops(const uint32_t (&q)[4], int, h8& b0, h8& b1) {
-        b0 = byte8(q[0] ^ 0x80808080u, q[1] ^ 0x80808080u, (_Float16)1152.0f);
-        b1 = byte8(q[2] ^ 0x80808080u, q[3] ^ 0x80808080u, (_Float16)1152.0f);
+        b0 = byte8(q[0], q[1], (_Float16)1056.0f);
+        b1 = byte8(q[2], q[3], (_Float16)1056.0f);
     }
 };
 
@@ -699,52 +699,49 @@ __global__ __launch_bounds__(512) void mmqp_kernel(MmqArgs a, int steps_per_spli
 // 128 h + 32 k + l of a super-block is nibble k / 2 of ql[64 h + 32 (k % 2)
 // + l] with bits 2 k, 2 k + 1 of qh[32 h + l] on top, minus 32, scale
 // sc[8 h + 2 k + l / 16]) -> 36-byte blocks of 32 elements (PB<Q6_K>): d,
-// the block's two sub-block scales, the 32 codes as int8, bytes 8 g .. 8 g +
-// 7 of each 16 holding elements 8 g .. of sub-block 0 then of sub-block 1.
-// One thread per block; its 32 ql and 32 qh bytes are read as 16-byte loads
-// from their 2-byte-aligned addresses (gfx950 serves unaligned loads).
+// the block's two sub-block scales, the 32 codes 0..63, bytes 8 g .. 8 g + 7
+// of each 16 holding elements 8 g .. of sub-block 0 then of sub-block 1 --
+// in dwords of four codes, the element dwords 0, 1, 4, 5, 2, 3, 6, 7.
+// One thread per half super-block (the four blocks k = 0..3 of half h share
+// its 32 qh bytes and two 32-byte ql runs): six 16-byte loads from the
+// 2-byte-aligned GGUF bytes (gfx950 serves unaligned loads) and the 144
+// output bytes as nine 16-byte stores (a half super-block's output starts
+// on a multiple of 144 bytes, rows being 288 bytes per super-block).
 __global__ __launch_bounds__(256) void q6c_kernel(const uint8_t* __restrict__ w, int N, int K,
                                                   int64_t row_bytes, uint8_t* __restrict__ out) {
-    const int nb = K / 32;
-    const size_t total = (size_t)N * nb;
+    const int nh = K / 128;  // half super-blocks per row
+    const size_t total = (size_t)N * nh;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
          i += (size_t)gridDim.x * 256) {
-        const int n = (int)(i / nb), bi = (int)(i - (size_t)n * nb);
-        const int sbi = bi >> 3, h = (bi >> 2) & 1, k = bi & 3;
-        const uint8_t* sb = w + (size_t)n * row_bytes + (size_t)210 * sbi;
-        const uint4* qlp = reinterpret_cast<const uint4*>(sb + 64 * h + 32 * (k & 1));
+        const int n = (int)(i / nh), u = (int)(i - (size_t)n * nh);
+        const int h = u & 1;
+        const uint8_t* sb = w + (size_t)n * row_bytes + (size_t)210 * (u >> 1);
+        const uint4* qlp = reinterpret_cast<const uint4*>(sb + 64 * h);
         const uint4* qhp = reinterpret_cast<const uint4*>(sb + 128 + 32 * h);
-        const uint4 l0 = qlp[0], l1 = qlp[1], h0 = qhp[0], h1 = qhp[1];
-        const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-        const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-        const uint16_t sc = *reinterpret_cast<const uint16_t*>(sb + 192 + 8 * h + 2 * k);
-        const uint16_t d = *reinterpret_cast<const uint16_t*>(sb + 208);
-        uint8_t c[32];  // codes in element order, + 128 offset removed below
+        const uint4 l0 = qlp[0], l1 = qlp[1], l2 = qlp[2], l3 = qlp[3], h0 = qhp[0], h1 = qhp[1];
+        const uint32_t L[2][8] = {{l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w},
+                                  {l2.x, l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w}};
+        const uint32_t H[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        const uint32_t s01 = *reinterpret_cast<const uint32_t*>(sb + 192 + 8 * h),
+                       s23 = *reinterpret_cast<const uint32_t*>(sb + 196 + 8 * h);
+        const uint32_t d = *reinterpret_cast<const uint16_t*>(sb + 208);
+        uint32_t o[36];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t sc = k < 2 ? (s01 >> (16 * k)) & 0xFFFFu : (s23 >> (16 * (k - 2))) & 0xFFFFu;
+            o[9 * k] = d | (sc << 16);
+            constexpr int ED[8] = {0, 1, 4, 5, 2, 3, 6, 7};  // element dword of output dword p
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const uint32_t nib = ((lw[u] >> (8 * v)) >> (4 * (k >> 1))) & 0xFu;
-                const uint32_t hb = ((hw[u] >> (8 * v)) >> (2 * k)) & 0x3u;
-                c[4 * u + v] = (uint8_t)((int)(nib | (hb << 4)) - 32);
+            for (int p = 0; p < 8; ++p) {
+                const int j = ED[p];
+                const uint32_t nib = (L[k & 1][j] >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
+                const uint32_t hb = (H[j] >> (2 * k)) & 0x03030303u;
+                o[9 * k + 1 + p] = nib | (hb << 4);
             }
         }
-        uint32_t o[9];
-        o[0] = (uint32_t)d | ((uint32_t)sc << 16);
+        uint4* dst = reinterpret_cast<uint4*>(out + i * 144);
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {  // dword p: bytes 4 p .. 4 p + 3 of the code area
-            uint32_t v = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int q = 4 * p + b;  // byte q holds element e (layout above)
-                const int e = (q & 7) + 8 * ((q >> 4) & 1) + 16 * ((q >> 3) & 1);
-                v |= (uint32_t)c[e] << (8 * b);
-            }
-            o[1 + p] = v;
-        }
-        uint32_t* dst = reinterpret_cast<uint32_t*>(out + i * 36);
-#pragma unroll
-        for (int p = 0; p < 9; ++p) dst[p] = o[p];
+        for (int p = 0; p < 9; ++p) dst[p] = make_uint4(o[4 * p], o[4 * p + 1], o[4 * p + 2], o[4 * p + 3]);
     }
 }
 
@@ -759,7 +756,7 @@ int64_t mmqp_q6c_bytes(int N, int K) { return (int64_t)N * (K / 32) * 36; }
 
 hipError_t launch_q6c(const uint8_t* w, int N, int K, int64_t row_bytes, uint8_t* out,
                       hipStream_t st) {
-    const size_t total = (size_t)N * (K / 32);
+    const size_t total = (size_t)N * (K / 128);
     const int grid = (int)std::min<size_t>((total + 255) / 256, 16384);
     hipLaunchKernelGGL(q6c_kernel, dim3(grid), dim3(256), 0, st, w, N, K, row_bytes, out);
     return hipGetLastError();
