@@ -550,10 +550,13 @@ constexpr int DPG_DEEP = 3;  // the deepest of deep_depth<F>() (launch geometry)
 constexpr int DEEP_ROWS = 65536;
 
 // Two lane units per lane hold both units' activation limbs in registers:
-// more than the 128 VGPRs of a 1024-thread work-group, so they run 512.
+// more than the 128 VGPRs of a 1024-thread work-group, so they run 512.  With
+// half the waves per CU they keep two steps of loads in flight (132-135
+// VGPRs): Q4_0 3584 x 18944 14.7 -> 14.1 us aligned, 16.3 -> 15.3 GGUF;
+// three steps measured slower (15.5 / 16.8).
 template <int NL>
 constexpr int depth() {
-    return DP;
+    return NL == 2 ? 2 : DP;
 }
 template <int NL, int WG>
 constexpr int nl_wg() {
