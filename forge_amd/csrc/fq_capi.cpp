@@ -1,11 +1,15 @@
 // fq_capi.cpp -- the extern "C" entry points declared in include/forge_q.h:
 // argument validation, launch planning and the per-stream scratch memory.
 //
-// M == 1 runs the batch-1 GEMV kernels (fq_gemv1.hip on GGUF bytes,
-// fq_gemvp.hip on the aligned layout); every M > 1 -- the reference's
-// batched GEMV (1 < M <= 32) and its dequant + GEMM prefill (M > 32),
-// matmul.cpp:1150-1286 -- runs the MFMA kernels of fq_mmq.hip, which pick
-// their tile shape from M.
+// Dispatch by token count (run_matmul): M = 1 runs the batch-1 GEMV kernels
+// (fq_gemvp.hip / fq_gemvt.hip over GGUF bytes or the aligned layout, the
+// row-step kernels of fq_gemv1.hip under about 8 MB of weights); M = 2..4
+// the same batch-1 kernels with each weight unit dotted with every token;
+// Q4_K M = 4..16 the band kernel of fq_mmqs.hip; M > 32 the prefill kernel
+// of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --
+// the reference's batched GEMV (1 < M <= 32) and dequant + GEMM prefill
+// (M > 32), matmul.cpp:1150-1286 -- the int8 and fp16 MFMA kernels of
+// fq_mmqi.hip and fq_mmq.hip.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -191,8 +195,19 @@ int mmqs_plan(int N, int K, int cus, int* rows_per_wg) {
     return 1;
 }
 
-// Workspace bytes and K-splits of the Q8_0 / Q4_0 prefill kernel (M > 32,
-// K a multiple of 256): one work-group per CU and tile, K split when that
+// Workspace bytes of a band-kernel call: the token operands of plan_mmq's
+// single token tile and, when K is split, the slabs.
+size_t mmqs_need(int M, int K, int N, int cus) {
+    const MmqPlan pl = plan_mmq(M, K, N, cus);
+    int rpw = 0;
+    const int splits = mmqs_plan(N, K, cus, &rpw);
+    const size_t part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    return 256 + al(pl.xop_b) + al(pl.xsum_b) + al(pl.ex_b) + al(part_b);
+}
+
+// Workspace bytes and K-splits of the prefill kernel (M > 32, K a multiple
+// of 256): one work-group per CU and tile, K split when that
 // shortens the busiest CU's work, each split a multiple of four 64-element
 // steps.
 struct MmqpPlan {
@@ -370,8 +385,7 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
         int rpw = 0;
         const int splits = mmqs_plan(N, K, di.cus, &rpw);
-        const size_t part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;
-        const size_t need = 256 + al(pl.xop_b) + al(pl.xsum_b) + al(pl.ex_b) + al(part_b);
+        const size_t need = mmqs_need(M, K, N, di.cus);
         std::unique_ptr<StreamScratch::Lease> lease;
         uint8_t* buf = fixed;
         if (fixed) {
@@ -1056,12 +1070,13 @@ int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
     // slot 0: the largest MFMA-path plan for up to M_max tokens (the split-K
     // slabs grow with splits x N, and fewer rows can mean more splits: every
     // row count that changes the tile count is tried, with K_max and, for the
-    // Q8_0 / Q4_0 prefill kernel, the largest multiple of 256 up to K_max)
+    // prefill and band kernels, the largest multiple of 256 up to K_max)
     size_t need0 = 0;
     const int Kp = K_max - K_max % 256;
     for (int n = N_max; n > 0; n = n > 128 ? ((n - 1) / 128) * 128 : 0) {
         for (int m = 2; m <= M_max; ++m) {
             need0 = std::max(need0, plan_mmq(m, K_max, n, di.cus).total);
+            if (m >= 4 && m <= 16 && Kp > 0) need0 = std::max(need0, mmqs_need(m, Kp, n, di.cus));
             if (m > 32 && Kp > 0) need0 = std::max(need0, plan_mmqp(m, Kp, n, di.cus, true).total);
         }
     }

@@ -716,15 +716,15 @@ __global__ __launch_bounds__(256) void q6c_kernel(const uint8_t* __restrict__ w,
         const int n = (int)(i / nh), u = (int)(i - (size_t)n * nh);
         const int h = u & 1;
         const uint8_t* sb = w + (size_t)n * row_bytes + (size_t)210 * (u >> 1);
-        const uint4* qlp = reinterpret_cast<const uint4*>(sb + 64 * h);
-        const uint4* qhp = reinterpret_cast<const uint4*>(sb + 128 + 32 * h);
-        const uint4 l0 = qlp[0], l1 = qlp[1], l2 = qlp[2], l3 = qlp[3], h0 = qhp[0], h1 = qhp[1];
+        const uint8_t* qlp = sb + 64 * h;
+        const uint8_t* qhp = sb + 128 + 32 * h;
+        const uint4 l0 = ld_u128(qlp), l1 = ld_u128(qlp + 16), l2 = ld_u128(qlp + 32),
+                    l3 = ld_u128(qlp + 48), h0 = ld_u128(qhp), h1 = ld_u128(qhp + 16);
         const uint32_t L[2][8] = {{l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w},
                                   {l2.x, l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w}};
         const uint32_t H[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-        const uint32_t s01 = *reinterpret_cast<const uint32_t*>(sb + 192 + 8 * h),
-                       s23 = *reinterpret_cast<const uint32_t*>(sb + 196 + 8 * h);
-        const uint32_t d = *reinterpret_cast<const uint16_t*>(sb + 208);
+        const uint32_t s01 = ld_u32(sb + 192 + 8 * h), s23 = ld_u32(sb + 196 + 8 * h);
+        const uint32_t d = ld_u16(sb + 208);
         uint32_t o[36];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
