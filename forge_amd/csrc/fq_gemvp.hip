@@ -24,29 +24,59 @@ namespace {
 template <int F>
 struct Pk;
 
+// The 4-bit formats take nibble records (fq_limbs.h): code dword k holds
+// elements 4 k, 4 k + 16, 4 k + 1, ... in nibble order, as do the records'
+// hex digits, so v_dot8_i32_i4 multiplies them in place.  q ^ 8 is the code
+// q - 8 as a signed nibble; E = sum (q - 8) n over the unit, in three
+// independent chains over digit pairs (2 j + 1, 2 j): P_j = 16 D_{2j+1} +
+// D_{2j}, then E = 2^16 P_2 + 2^8 P_1 + P_0 (|E| < 32 * 8 * 2^22).
+__device__ __forceinline__ int nib_dot(const uint4& qs, const Limbs& L) {
+    const int w[4] = {(int)(qs.x ^ 0x88888888u), (int)(qs.y ^ 0x88888888u),
+                      (int)(qs.z ^ 0x88888888u), (int)(qs.w ^ 0x88888888u)};
+    const int* lim[3] = {L.l1, L.l2, L.l3};  // pair j: digits 2 j (dwords 0..3), 2 j + 1 (4..7)
+    int P[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        int e = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) e = __builtin_amdgcn_sdot8(w[k], lim[j][4 + k], e, false);
+        e *= 16;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) e = __builtin_amdgcn_sdot8(w[k], lim[j][k], e, false);
+        P[j] = e;
+    }
+    return P[2] * 65536 + P[1] * 256 + P[0];
+}
+
 template <>
 struct Pk<Q4_0> {
     static constexpr int NREC = 1, NG = 1;
+    static constexpr bool NIB = true;
     using Raw = Fmt<Q4_0>::Raw;
     __device__ static int k_of(int w, int s) { return 32 * w + s; }
     __device__ static Raw load(const uint8_t* row, int v, int U) {
         return Raw{ldg16<true>(row + 16 * U + 2 * v), ldg128<true>(row + 16 * v)};
     }
-    __device__ static float dot(const Raw& r, int v, const Limbs* L) {
-        return limb_dot<Q4_0>(r, v, L[0]);
+    // d (q - 8) . x = d s1 E
+    __device__ static float dot(const Raw& r, int, const Limbs* L) {
+        return f16_hw(r.d) * L[0].s1 * (float)nib_dot(r.qs, L[0]);
     }
 };
 
 template <>
 struct Pk<Q4_1> {
     static constexpr int NREC = 1, NG = 1;
+    static constexpr bool NIB = true;
     using Raw = Fmt<Q4_1>::Raw;
     __device__ static int k_of(int w, int s) { return 32 * w + s; }
     __device__ static Raw load(const uint8_t* row, int v, int U) {
         return Raw{ldg32<true>(row + 16 * U + 4 * v), ldg128<true>(row + 16 * v)};
     }
-    __device__ static float dot(const Raw& r, int v, const Limbs* L) {
-        return limb_dot<Q4_1>(r, v, L[0]);
+    // (d q + m) . x = d s1 E + (8 d + m) S
+    __device__ static float dot(const Raw& r, int, const Limbs* L) {
+        const float d = f16_hw(r.dm & 0xFFFFu), m = f16_hw(r.dm >> 16);
+        return __builtin_fmaf(d * L[0].s1, (float)nib_dot(r.qs, L[0]),
+                              __builtin_fmaf(8.0f, d, m) * L[0].S[0]);
     }
 };
 
@@ -379,7 +409,9 @@ __device__ __forceinline__ Step step_of(int f, int rows, float inv_rows) {
 // the next loads are issued into the freed registers, then each lane reads
 // its unit from the buffer.  A wave's LDS accesses execute in order, so no
 // barrier separates the writes from the reads.
-template <int F, int NL, int MODE, int GP, int NT>
+// Limb reloads: RL 0 never (rows of one K-slice: loaded before the loop),
+// 1 when the step's slice differs from the wave's last, 2 every step.
+template <int F, int NL, int MODE, int GP, int NT, int RL>
 __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& st, int& nxt,
                                       const Claims& cl, const GemvArgs& a,
                                       Limbs (&L)[NT][NL][Pk<F>::NREC], const uint8_t* lds,
@@ -388,7 +420,7 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& 
     const Step cp = st;
     st = step_of(nxt, cl.rows, cl.inv_rows);
     if (nxt >= 0) nxt = claim(cl, lane);  // wave-uniform
-    if (cp.f >= 0 && cp.s != cur_s) {  // wave-uniform
+    if (RL == 2 || (RL == 1 && cp.f >= 0 && cp.s != cur_s)) {  // wave-uniform
 #pragma unroll
         for (int t = 0; t < NT; ++t)
             load_slice_limbs<F, NL>(L[t], lds + (size_t)t * a.Uc * RECB, cp.s, a.U, lane);
@@ -446,7 +478,8 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& 
 // read and decoded once is dotted with each token's limbs; token t's records
 // follow token t - 1's, and y, the partial sums and a full bias
 // (a.bias_mode 2) are token-major.
-template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE, int GP = 0, int NT = 1>
+template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE, int GP = 0, int NT = 1,
+          bool OS = false>
 __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     static_assert(NT == 1 || (MODE == ONE && GP > 0), "several tokens: GGUF rows, MODE ONE");
     constexpr bool DUAL = MODE == PAIR;
@@ -502,11 +535,23 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     // of loads in flight at the loop head is always the same and the compiler
     // waits for exactly one slot's loads (a skipped load would make it drain
     // the whole queue); steps are claimed in order, so once slot 0 holds no
-    // step neither does any later slot
+    // step neither does any later slot.  The wave reloads its limbs when the
+    // slice changes.  For the nibble records (4-bit formats) that conditional
+    // reload leaves the compiler copying all the limb registers at the loop's
+    // back edge (about 50 VALU instructions per iteration), so their kernels
+    // come in two forms: rows of one K-slice (OS) load the limbs once, longer
+    // rows reload them at every step (the LDS reads cost less).
+    constexpr int RL = !NibRec<P>::value ? 1 : OS ? 0 : 2;
+    if constexpr (RL == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            load_slice_limbs<F, NL>(L[t], lds + (size_t)t * a.Uc * RECB, 0, a.U, lane);
+    }
     while (st[0].f >= 0) {
 #pragma unroll
         for (int j = 0; j < D; ++j)
-            pstep<F, NL, MODE, GP, NT>(f[j], st[j], nxt, cl, a, L, lds, wbuf, part, lo, lane, cur_s);
+            pstep<F, NL, MODE, GP, NT, RL>(f[j], st[j], nxt, cl, a, L, lds, wbuf, part, lo, lane,
+                                           cur_s);
     }
     __syncthreads();
     if constexpr (DUAL) {
@@ -563,25 +608,35 @@ constexpr int nl_wg() {
     return NL == 2 ? 512 : WG;
 }
 
+// The kernel's address; os: rows of one K-slice (its own form for the 4-bit
+// formats, whose limbs are then loaded once).
+template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE, int GP = 0, int NT = 1>
+const void* kfn(bool os) {
+    if constexpr (F == Q4_0 || F == Q4_1)
+        if (os)
+            return reinterpret_cast<const void*>(&gemvp_kernel<F, NL, D, BIAS, WG, MODE, GP, NT, true>);
+    return reinterpret_cast<const void*>(&gemvp_kernel<F, NL, D, BIAS, WG, MODE, GP, NT>);
+}
+
 template <int F, int NL>
-const void* pfn2(bool bias) {
+const void* pfn2(bool bias, bool os) {
     constexpr int WG = nl_wg<NL, WGP>();
-    return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, depth<NL>(), true, WG>)
-                : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, depth<NL>(), false, WG>);
+    return bias ? kfn<F, NL, depth<NL>(), true, WG>(os) : kfn<F, NL, depth<NL>(), false, WG>(os);
 }
 
 template <int F>
 const void* pfn(int units, bool bias, int* nl) {
     *nl = lane_units<F>(units);
+    const bool os = units <= 64 * *nl;
     if constexpr (F == Q4_0 || F == Q4_1)
-        if (*nl == 2) return pfn2<F, 2>(bias);
-    return pfn2<F, 1>(bias);
+        if (*nl == 2) return pfn2<F, 2>(bias, os);
+    return pfn2<F, 1>(bias, os);
 }
 
 template <int F>
-const void* pfn_mode(int mode) {
-    return mode == PAIR ? reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WGP, PAIR>)
-                        : reinterpret_cast<const void*>(&gemvp_kernel<F, 1, DP, false, WGP, CAT>);
+const void* pfn_mode(int mode, int units) {
+    const bool os = units <= 64;
+    return mode == PAIR ? kfn<F, 1, DP, false, WGP, PAIR>(os) : kfn<F, 1, DP, false, WGP, CAT>(os);
 }
 
 // GGUF rows: GP pieces per lane cover a K-slice; only the counts a format's
@@ -601,37 +656,38 @@ constexpr int gwg() {
 }
 
 template <int F, int NL, int GP, int D>
-const void* gfn3(bool bias) {
+const void* gfn3(bool bias, bool os) {
     constexpr int WG = nl_wg<NL, gwg<GP, D>()>();
-    return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, D, true, WG, ONE, GP>)
-                : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, D, false, WG, ONE, GP>);
+    return bias ? kfn<F, NL, D, true, WG, ONE, GP>(os) : kfn<F, NL, D, false, WG, ONE, GP>(os);
 }
 
 template <int F, int NL, int GP>
-const void* gfn2(bool bias, bool deep) {
+const void* gfn2(bool bias, bool deep, bool os) {
     if constexpr (GP > max_pieces<F>() * NL) {
         return nullptr;
     } else {
-        return deep ? gfn3<F, NL, GP, deep_depth<F>()>(bias) : gfn3<F, NL, GP, depth<NL>()>(bias);
+        return deep ? gfn3<F, NL, GP, deep_depth<F>()>(bias, os)
+                    : gfn3<F, NL, GP, depth<NL>()>(bias, os);
     }
 }
 
 template <int F>
 const void* gfn(int units, bool bias, bool deep, int* gp, int* nl) {
     *nl = lane_units<F>(units);
+    const bool os = units <= 64 * *nl;
     *gp = slice_pieces<F>(units < 64 * *nl ? units : 64 * *nl);
     if constexpr (F == Q4_0 || F == Q4_1) {
         if (*nl == 2) switch (*gp) {
-            case 2: return gfn2<F, 2, 2>(bias, deep);
-            case 3: return gfn2<F, 2, 3>(bias, deep);
+            case 2: return gfn2<F, 2, 2>(bias, deep, os);
+            case 3: return gfn2<F, 2, 3>(bias, deep, os);
             default: return nullptr;
         }
     }
     switch (*gp) {
-        case 1: return gfn2<F, 1, 1>(bias, deep);
-        case 2: return gfn2<F, 1, 2>(bias, deep);
-        case 3: return gfn2<F, 1, 3>(bias, deep);
-        case 4: return gfn2<F, 1, 4>(bias, deep);
+        case 1: return gfn2<F, 1, 1>(bias, deep, os);
+        case 2: return gfn2<F, 1, 2>(bias, deep, os);
+        case 3: return gfn2<F, 1, 3>(bias, deep, os);
+        case 4: return gfn2<F, 1, 4>(bias, deep, os);
         default: return nullptr;
     }
 }
@@ -650,36 +706,37 @@ constexpr int wg_t() {
 }
 
 template <int F, int NL, int GP, int NT>
-const void* gfn_t(bool bias) {
+const void* gfn_t(bool bias, bool os) {
     if constexpr (GP > max_pieces<F>() * NL) {
         return nullptr;
     } else {
         constexpr int WG = wg_t<NL, NT>();
-        return bias ? reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, true, WG, ONE, GP, NT>)
-                    : reinterpret_cast<const void*>(&gemvp_kernel<F, NL, DP, false, WG, ONE, GP, NT>);
+        return bias ? kfn<F, NL, DP, true, WG, ONE, GP, NT>(os)
+                    : kfn<F, NL, DP, false, WG, ONE, GP, NT>(os);
     }
 }
 
 template <int F, int NT>
 const void* gfnt(int units, bool bias, int* gp, int* nl) {
     *nl = lane_units<F>(units);
+    const bool os = units <= 64 * *nl;
     *gp = slice_pieces<F>(units < 64 * *nl ? units : 64 * *nl);
     if constexpr (F == Q4_0 || F == Q4_1) {
         if (*nl == 2) {
             if constexpr (NT == 2) {
                 switch (*gp) {
-                    case 2: return gfn_t<F, 2, 2, NT>(bias);
-                    case 3: return gfn_t<F, 2, 3, NT>(bias);
+                    case 2: return gfn_t<F, 2, 2, NT>(bias, os);
+                    case 3: return gfn_t<F, 2, 3, NT>(bias, os);
                 }
             }
             return nullptr;
         }
     }
     switch (*gp) {
-        case 1: return gfn_t<F, 1, 1, NT>(bias);
-        case 2: return gfn_t<F, 1, 2, NT>(bias);
-        case 3: return gfn_t<F, 1, 3, NT>(bias);
-        case 4: return gfn_t<F, 1, 4, NT>(bias);
+        case 1: return gfn_t<F, 1, 1, NT>(bias, os);
+        case 2: return gfn_t<F, 1, 2, NT>(bias, os);
+        case 3: return gfn_t<F, 1, 3, NT>(bias, os);
+        case 4: return gfn_t<F, 1, 4, NT>(bias, os);
         default: return nullptr;
     }
 }
@@ -702,24 +759,24 @@ const void* gfn_tokens(int tokens, int units, bool bias, int* gp, int* nl) {
 // The fused forms (MODE PAIR: gate/up; CAT: QKV) over GGUF rows: one lane
 // unit per lane, one step of loads in flight.
 template <int F, int MODE, int GP>
-const void* gfn_mode3() {
+const void* gfn_mode3(bool os) {
     if constexpr (GP > max_pieces<F>()) {
         return nullptr;
     } else {
-        return reinterpret_cast<const void*>(
-            &gemvp_kernel<F, 1, DP, false, gwg<GP, DP>(), MODE, GP>);
+        return kfn<F, 1, DP, false, gwg<GP, DP>(), MODE, GP>(os);
     }
 }
 
 template <int F>
 const void* gfn_mode(int mode, int units, int* gp) {
     *gp = slice_pieces<F>(units < 64 ? units : 64);
+    const bool os = units <= 64;
     const bool pair = mode == PAIR;
     switch (*gp) {
-        case 1: return pair ? gfn_mode3<F, PAIR, 1>() : gfn_mode3<F, CAT, 1>();
-        case 2: return pair ? gfn_mode3<F, PAIR, 2>() : gfn_mode3<F, CAT, 2>();
-        case 3: return pair ? gfn_mode3<F, PAIR, 3>() : gfn_mode3<F, CAT, 3>();
-        case 4: return pair ? gfn_mode3<F, PAIR, 4>() : gfn_mode3<F, CAT, 4>();
+        case 1: return pair ? gfn_mode3<F, PAIR, 1>(os) : gfn_mode3<F, CAT, 1>(os);
+        case 2: return pair ? gfn_mode3<F, PAIR, 2>(os) : gfn_mode3<F, CAT, 2>(os);
+        case 3: return pair ? gfn_mode3<F, PAIR, 3>(os) : gfn_mode3<F, CAT, 3>(os);
+        case 4: return pair ? gfn_mode3<F, PAIR, 4>(os) : gfn_mode3<F, CAT, 4>(os);
     }
     return nullptr;
 }
@@ -745,11 +802,11 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
     const void* fn = nullptr;
     *nl = 1;
     switch (dtype) {
-        case Q4_0: fn = mode ? pfn_mode<Q4_0>(mode) : pfn<Q4_0>(units, bias, nl); break;
-        case Q4_1: fn = mode ? pfn_mode<Q4_1>(mode) : pfn<Q4_1>(units, bias, nl); break;
-        case Q8_0: fn = mode ? pfn_mode<Q8_0>(mode) : pfn<Q8_0>(units, bias, nl); break;
-        case Q4_K: fn = mode ? pfn_mode<Q4_K>(mode) : pfn<Q4_K>(units, bias, nl); break;
-        case Q6_K: fn = mode ? pfn_mode<Q6_K>(mode) : pfn<Q6_K>(units, bias, nl); break;
+        case Q4_0: fn = mode ? pfn_mode<Q4_0>(mode, units) : pfn<Q4_0>(units, bias, nl); break;
+        case Q4_1: fn = mode ? pfn_mode<Q4_1>(mode, units) : pfn<Q4_1>(units, bias, nl); break;
+        case Q8_0: fn = mode ? pfn_mode<Q8_0>(mode, units) : pfn<Q8_0>(units, bias, nl); break;
+        case Q4_K: fn = mode ? pfn_mode<Q4_K>(mode, units) : pfn<Q4_K>(units, bias, nl); break;
+        case Q6_K: fn = mode ? pfn_mode<Q6_K>(mode, units) : pfn<Q6_K>(units, bias, nl); break;
     }
     if (mode) *nl = 1;
     *lds = (size_t)records * RECB;

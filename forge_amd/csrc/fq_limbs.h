@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fq_formats.h"
 
 namespace fq {
@@ -140,8 +142,75 @@ __device__ __forceinline__ LimbQuad limb_quad(float4 xv) {
                     pack4(a3[0], a3[1], a3[2], a3[3]), s1, gs};
 }
 
+// Nibble records (record traits with NIB = true: the 4-bit formats, dotted
+// with v_dot8_i32_i4).  The unit's activations become n = rint(x / s1),
+// s1 = 2^(ilogb(max |x|) - 21), so |n| < 2^22, held as six signed hex digits
+// n = sum_i a_i 16^i, a_i in [-8, 7] (from u = n + 0x888888, whose nibble i
+// is a_i + 8).  Limb i takes bytes 16 i .. 16 i + 15 of the record, dword k
+// holding the digits of elements 4 k, 4 k + 16, 4 k + 1, 4 k + 17, ... in
+// nibble order: the order of a 16-byte block of low / high code nibbles.
+// s1 @96 and the unit sum S @100 as in the byte records.
+template <class Fm, class = void>
+struct NibRec : std::false_type {};
+template <class Fm>
+struct NibRec<Fm, std::void_t<decltype(Fm::NIB)>> : std::bool_constant<Fm::NIB> {};
+
+__device__ __forceinline__ void build_nib(uint8_t* rec, float4 xv, int i, bool live) {
+    float m = fmaxf(fmaxf(__builtin_fabsf(xv.x), __builtin_fabsf(xv.y)),
+                    fmaxf(__builtin_fabsf(xv.z), __builtin_fabsf(xv.w)));
+    m = group_max8(m);
+    const int e = max((int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu), 22);
+    float s1 = __builtin_bit_cast(float, (uint32_t)(e - 21) << 23);
+    const float inv = __builtin_bit_cast(float, (uint32_t)(275 - e) << 23);
+    const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+    // v = u ^ 0x888888: nibble i of v is digit a_i as a signed nibble
+    uint32_t v[4], pv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        v[j] = (uint32_t)((int)__builtin_rintf(xs[j] * inv) + 0x888888) ^ 0x888888u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)  // lane i ^ 4 of the unit (ds_swizzle, xor mask 4)
+        pv[j] = (uint32_t)__builtin_amdgcn_ds_swizzle((int)v[j], 0x101F);
+    if (!(m <= 3.0e38f)) s1 = __builtin_nanf("");  // Inf/NaN in x propagates
+    float gs = (xv.x + xv.y) + (xv.z + xv.w);
+    gs = group_sum<8>(gs);
+    if (!live) return;
+    // lanes 0..3 hold elements 4 i .. 4 i + 3 and write dword i of limbs 0..3
+    // (bytes 0, 1 of v); lanes 4..7 hold elements 16 + 4 (i - 4) .. and write
+    // dword i - 4 of limbs 4, 5 (byte 2)
+    const bool low = i < 4;
+    const uint32_t* lo = low ? v : pv;
+    const uint32_t* hi = low ? pv : v;
+    auto gather = [](const uint32_t* q, int b) {  // byte b of q[0..3] as one dword
+        const uint32_t sel = (uint32_t)b | ((uint32_t)(4 + b) << 8) | 0x0C0C0000u;
+        const uint32_t t01 = __builtin_amdgcn_perm(q[1], q[0], sel);
+        const uint32_t t23 = __builtin_amdgcn_perm(q[3], q[2], sel);
+        return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+    };
+    uint32_t* r = reinterpret_cast<uint32_t*>(rec) + (i & 3);
+    auto put = [&](int b) {  // limbs 2 b (low nibbles) and 2 b + 1 (high nibbles)
+        const uint32_t xl = gather(lo, b), xh = gather(hi, b);
+        r[4 * (2 * b)] = (xl & 0x0F0F0F0Fu) | ((xh << 4) & 0xF0F0F0F0u);
+        r[4 * (2 * b + 1)] = ((xl >> 4) & 0x0F0F0F0Fu) | (xh & 0xF0F0F0F0u);
+    };
+    if (low) {
+        put(0);
+        put(1);
+    } else {
+        put(2);
+    }
+    if (i == 0) {
+        *reinterpret_cast<float*>(rec + 96) = s1;
+        *reinterpret_cast<float*>(rec + 100) = gs;
+    }
+}
+
 template <class Fm>
 __device__ __forceinline__ void build_task(uint8_t* lds, float4 xv, int t, int tasks) {
+    if constexpr (NibRec<Fm>::value) {
+        build_nib(lds + RECB * (t >> 3), xv, t & 7, t < tasks);
+        return;
+    }
     constexpr int NG = Fm::NG, GS = 32 / NG;
     const int i = t & 7;
     const LimbQuad lq = limb_quad<GS>(xv);
