@@ -349,12 +349,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     }
 
     if (M == 1 && K > 0 && packable(dtype) &&
-        (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
+        (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (4 << 20))) {
         // batch 1 on the five benchmark formats: the aligned-layout kernel,
         // reading the GGUF rows through per-wave LDS buffers (with one token a
-        // full [1][N] bias is a row vector of N).  Below ~8 MB of weights the
-        // row-step and chunk kernels start faster (TinyLlama shapes: 3.7 us
-        // against 5.3 us for 2048 x 2048 Q4_0); Q6_K always runs here.
+        // full [1][N] bias is a row vector of N).  Below ~4 MB of weights the
+        // row-step kernels start faster (2048 x 2048 Q4_0, 2.4 MB: 3.6 us
+        // against 4.2); from 4.5 MB this one is (2048 x 2048 Q8_0 4.4 against
+        // 4.7 us, TinyLlama Q4_0 5632 x 2048 4.8 against 5.15); Q6_K always
+        // runs here.
         const int rc = packed_gemv(dtype, x, w, nullptr, nullptr, 0, 0, 0,
                                    bias_mode ? bias : nullptr, bias_mode == 2 ? N : bias_len, y,
                                    K, N, st, true);
