@@ -1,7 +1,8 @@
 // fq_gemvt.hip -- batch-1 GEMV over the tiled aligned layout, one matrix row
-// per lane: Q4_0, Q4_1 and Q8_0 matrices of at least TILED_MIN_ROWS rows
-// (fq_pack.h), the lm_head-type shapes where it beats the row-step kernel of
-// fq_gemvp.hip.
+// per lane: Q8_0 matrices of at least TILED_MIN_ROWS rows (fq_pack.h), the
+// lm_head-type shapes where it beats the K-sliced kernel of fq_gemvp.hip
+// (152064 x 3584: 87.5 against 97.5 us).  The 4-bit formats, whose K-sliced
+// kernel dots the code nibbles in place (v_dot8_i32_i4), run faster there.
 //
 // The tiled layout groups rows in tiles of 16, storing the 16-byte pieces
 // piece-major and row-minor, so pieces j .. j+3 of the tile's 16 rows are one
@@ -103,24 +104,6 @@ __device__ __forceinline__ void sums32(const Rec& r, const int (&q)[8], int& d1,
     d3 = e3;
 }
 
-// E = D1 2^14 + D2 2^7 + D3 over the 32 slots of a record for unsigned codes
-// of at most 15: |E| <= 32 * 15 * (127 * 2^14 + 64 * 2^7 + 64) < 2^31.
-__device__ __forceinline__ int chain32(const Rec& r, const int (&q)[8]) {
-    int d1, d2, d3;
-    sums32(r, q, d1, d2, d3);
-    return (d1 << 14) + (d2 << 7) + d3;
-}
-
-__device__ __forceinline__ void nib8(const uint4& w, int (&q)[8]) {
-    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        q[i] = (int)(v[i] & 0x0F0F0F0Fu);
-        q[4 + i] = (int)((v[i] >> 4) & 0x0F0F0F0Fu);
-    }
-}
-
-
 // Weight loads are raw buffer loads (one 32-bit address space per matrix,
 // bounds-checked by the hardware): the uniform part of an address -- the
 // tile's offset, the plane and the piece index times the tile's rows -- is the
@@ -168,51 +151,6 @@ __device__ __forceinline__ uint32_t pso(const TileRef& t, uint32_t o, uint32_t j
 // slot s of a record, NB register buffers in the load pipeline.
 template <int F>
 struct T;
-
-template <>
-struct T<Q4_0> {  // planes: qs (U x 16), d (U x 2, padded); unit = one block
-    static constexpr int NREC = 1, GS = 32, NB = 8;
-    struct Raw {
-        uint4 qs;
-        uint32_t d;
-    };
-    __device__ static int k_of(int w, int s) { return 32 * w + s; }
-    __device__ static void load(Raw& f, const TileRef& t, int r, int q, int g, int U) {
-        f.qs = bld128(t.b, pso(t, 0, 4 * g), 16 * (q * t.R + r));
-        // a d piece holds 8 units: this step is its half g & 1
-        f.d = bld16(t.b, pso(t, 16 * U, g >> 1), 16 * r + 2 * (4 * (g & 1) + q));
-    }
-    __device__ static float dot(const Raw& f, const Rec (&rr)[NREC], int) {
-        const Rec& rc = rr[0];
-        int q[8];
-        nib8(f.qs, q);
-        const float e = (float)chain32(rc, q);
-        const float v = __builtin_fmaf(e, rec_s1(rc) * 0x1p-14f, -8.0f * rec_S<0>(rc));
-        return f16_hw(f.d) * v;
-    }
-};
-
-template <>
-struct T<Q4_1> {  // planes: qs (U x 16), (d, m) (U x 4); unit = one block
-    static constexpr int NREC = 1, GS = 32, NB = 8;
-    struct Raw {
-        uint4 qs;
-        uint32_t dm;
-    };
-    __device__ static int k_of(int w, int s) { return 32 * w + s; }
-    __device__ static void load(Raw& f, const TileRef& t, int r, int q, int g, int U) {
-        f.qs = bld128(t.b, pso(t, 0, 4 * g), 16 * (q * t.R + r));
-        f.dm = bld32(t.b, pso(t, 16 * U, g), 16 * r + 4 * q);
-    }
-    __device__ static float dot(const Raw& f, const Rec (&rr)[NREC], int) {
-        const Rec& rc = rr[0];
-        int q[8];
-        nib8(f.qs, q);
-        const float e = (float)chain32(rc, q);
-        const float d = f16_hw(f.dm & 0xFFFFu), m = f16_hw(f.dm >> 16);
-        return __builtin_fmaf(d * (rec_s1(rc) * 0x1p-14f), e, m * rec_S<0>(rc));
-    }
-};
 
 template <>
 struct T<Q8_0> {  // planes: qs[0,16) (U x 16), qs[16,32) (U x 16), d (U x 2, padded)
@@ -479,8 +417,6 @@ int gemvt_tile_rows() { return TR; }
 
 const void* gemvt_kernel_fn(int dtype, int mode) {
     switch (dtype) {
-        case Q4_0: return tfn_mode<Q4_0>(mode);
-        case Q4_1: return tfn_mode<Q4_1>(mode);
         case Q8_0: return tfn_mode<Q8_0>(mode);
     }
     return nullptr;

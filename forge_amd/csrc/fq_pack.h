@@ -11,7 +11,7 @@
 //  - row-major: row n at n packed_row_bytes(K), its pieces in plane order;
 //    a batch-1 lane reads piece v of a row, so a wave's load moves 1 KiB of
 //    one row (fq_gemvp.hip);
-//  - 16-row tiles (Q4_0, Q4_1, Q8_0 with at least TILED_MIN_ROWS rows):
+//  - 16-row tiles (Q8_0 with at least TILED_MIN_ROWS rows):
 //    tile t starts at byte 16 t packed_row_bytes(K), and within a tile of R
 //    rows (the last tile holds the N mod 16 remaining rows) piece J of row r
 //    sits at (J R + r) 16.  Pieces J .. J+3 of the tile's rows are one
@@ -41,13 +41,14 @@ namespace fq {
 __host__ __device__ inline int64_t pad16(int64_t b) { return (b + 15) & ~(int64_t)15; }
 
 // The tiled arrangement: the one-row-per-lane kernel (fq_gemvt.hip) against
-// the one-row-per-step kernel (fq_gemvp.hip), 152064 x 3584, M = 1: Q4_0 53.5
-// against 67.8 us, Q4_1 55.9 / 70.4, Q8_0 88.3 / 97.9; the superblock
-// formats do not gain (Q4_K 55.2 / 55.0, Q6_K 77.4 / 69.1), nor do matrices
-// of fewer rows (Q4_0 18944 x 3584: 14.4 / 11.0).
+// the one-row-per-step kernel (fq_gemvp.hip), 152064 x 3584, M = 1: Q8_0 87.5
+// against 97.5 us.  The 4-bit formats, dotted nibble-in-place on the latter,
+// do better row-major (Q4_0 49.6 against 53.3 us, Q4_1 54.8 / 55.4, 65536 x
+// 4096 Q4_0 25.5 / 28.8); the superblock formats do not gain (Q4_K 55.2 /
+// 55.0, Q6_K 77.4 / 69.1), nor do matrices of fewer rows.
 constexpr int64_t TILED_MIN_ROWS = 65536;
 __host__ __device__ inline bool packed_tiled(int dtype, int64_t N) {
-    return (dtype == 2 || dtype == 3 || dtype == 7) && N >= TILED_MIN_ROWS;
+    return dtype == 7 && N >= TILED_MIN_ROWS;
 }
 
 // Packed row stride in bytes (0 when the format has no packed form).

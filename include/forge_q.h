@@ -124,10 +124,10 @@ int fq_dequant_rows(uint32_t dtype, const void* w, float* out, int N, int K, voi
  * the same bytes of each row, moved into 16-byte-aligned "planes" (the piece
  * a GEMV lane reads for lane unit v sits at plane + 16 v) followed by dense
  * scale arrays; the per-format layout is documented in forge_amd/csrc/fq_pack.h.
- * Rows are contiguous at a pitch of fq_packed_row_bytes, except for Q4_0,
- * Q4_1 and Q8_0 matrices of 65536 rows and more, whose rows are grouped in
- * tiles of 16 with their 16-byte pieces interleaved row by row (the batch-1
- * kernel there gives each lane one row).  The buffer size is the same either
+ * Rows are contiguous at a pitch of fq_packed_row_bytes, except for Q8_0
+ * matrices of 65536 rows and more, whose rows are grouped in tiles of 16
+ * with their 16-byte pieces interleaved row by row (the batch-1 kernel there
+ * gives each lane one row).  The buffer size is the same either
  * way (N * fq_packed_row_bytes), and the arrangement depends only on dtype
  * and N: a packed matrix is always used with the N it was packed with (a
  * row range of a tiled matrix is not a packed matrix of its own).

@@ -61,10 +61,10 @@ def test_fused_gguf(dtype, M):
     ("q8_0", F.Q8_0, 1000, 4096),
     ("q4_1-odd-n", F.Q4_1, 77, 2048),
     ("one-row", F.Q4_K, 1, 256),
-    # 65536 rows and more of Q4_0 / Q4_1 / Q8_0: the 16-row tiled arrangement
-    # (one row per lane), the last tile partial
-    ("q4_0-tiled", F.Q4_0, 65541, 512),
-    ("q8_0-tiled", F.Q8_0, 65536, 256),
+    # 65536 rows and more: Q8_0 takes the 16-row tiled arrangement (one row
+    # per lane, the last tile partial); Q4_0 stays row-major
+    ("q4_0-65541", F.Q4_0, 65541, 512),
+    ("q8_0-tiled", F.Q8_0, 65541, 256),
 ])
 def test_fused_packed(name, dtype, N, K):
     wg, wu = make(dtype, N, K, 7)
@@ -195,10 +195,13 @@ def test_fused_qkv_gguf(dtype, M):
     ("qwen7b-q4_k", F.Q4_K, 3584, 3584, 512, 512),
     ("q6_k-odd", F.Q6_K, 1024, 77, 0, 33),
     ("q8_0", F.Q8_0, 2048, 300, 50, 50),
-    # tiled Q (65536 rows and more) beside row-major K and V: one GEMV each
-    ("q4_0-mixed-arrangements", F.Q4_0, 256, 65541, 64, 40),
+    # tiled Q (Q8_0, 65536 rows and more) beside row-major K and V: one GEMV
+    # each
+    ("q8_0-mixed-arrangements", F.Q8_0, 256, 65541, 64, 40),
     # all three tiled: one launch over the three matrices
-    ("q4_1-all-tiled", F.Q4_1, 256, 65536, 65552, 65541),
+    ("q8_0-all-tiled", F.Q8_0, 256, 65536, 65552, 65541),
+    # 4-bit matrices of 65536 rows and more stay row-major: one launch
+    ("q4_1-65536-rows", F.Q4_1, 256, 65536, 65552, 65541),
 ])
 def test_fused_qkv_packed(name, dtype, K, Nq, Nk, Nv):
     ns = (Nq, Nk, Nv)

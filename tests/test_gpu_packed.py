@@ -28,7 +28,7 @@ def qweight(dtype, N, K, seed):
 
 @pytest.mark.parametrize("dtype", ALL)
 @pytest.mark.parametrize("N,K", [(1, 256), (37, 2048), (130, 3584), (9, 18944),
-                                 (65541, 256)])  # Q4_0/Q4_1/Q8_0: the tiled arrangement
+                                 (65541, 256)])  # Q8_0: the tiled arrangement
 def test_pack_roundtrip_bitexact(dtype, N, K):
     w, W = qweight(dtype, N, K, seed=N * 7 + K)
     P = ops.pack_weights(W)
@@ -70,10 +70,9 @@ def test_gemv_packed_configs(name, dtype, N, K):
 @pytest.mark.parametrize("N,K", [(1, 256), (7, 512), (65, 8192), (33, 12800),
                                  (65541, 256), (65536, 2048), (66000, 12800)])
 def test_gemv_packed_edges(dtype, N, K):
-    # 65536 rows and more of Q4_0, Q4_1 and Q8_0 take the tiled arrangement
-    # (the last tile partial at 65541 and 66000 rows; 66000 x 12800: the
-    # rows' records need 16 waves a work-group and the tiles more work-groups
-    # than CU slots)
+    # 65536 rows and more of Q8_0 take the tiled arrangement (the last tile
+    # partial at 65541 and 66000 rows; 66000 x 12800: the rows' records need
+    # 16 waves a work-group and the tiles more work-groups than CU slots)
     w, W = qweight(dtype, N, K, seed=3 * N + K)
     x = synth.make_x(1, K, seed=K + 1)
     y = ops.gemv_packed(torch.from_numpy(x).to(DEV), ops.pack_weights(W)).cpu().numpy()
