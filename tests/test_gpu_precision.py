@@ -39,6 +39,20 @@ def outlier_x(M, K, seed, kind):
     elif kind == "sparse":  # units of tiny values between units of huge ones
         u[:, 0::2, :] *= np.float32(1e4)
         u[:, 1::2, :] *= np.float32(1e-4)
+    elif kind == "edge":
+        # unit maxima just below and at powers of two (the largest float under
+        # 2^j rounds to the top of the representation's range: the 4-bit
+        # formats' hex digits then carry a top digit of 4), both signs, with
+        # the rest of the unit small and the unit's sign pattern varying
+        j = rng.integers(-6, 7, size=(M, K // 32)).astype(np.float32)
+        below = np.nextafter(np.float32(1.0), np.float32(0.0)) * np.exp2(j)
+        pos = rng.integers(0, 32, size=(M, K // 32))
+        sign = rng.choice([-1.0, 1.0], size=(M, K // 32)).astype(np.float32)
+        u *= np.float32(0.01) * np.exp2(j)[..., None]
+        val = np.where(rng.random((M, K // 32)) < 0.5, below, np.exp2(j)) * sign
+        np.put_along_axis(u, pos[..., None], val[..., None].astype(np.float32), axis=2)
+        np.put_along_axis(u, ((pos + 16) % 32)[..., None], (-val)[..., None].astype(np.float32),
+                          axis=2)
     return np.ascontiguousarray(x)
 
 
@@ -54,10 +68,11 @@ def check(dtype, w, x, N, K, y, what):
 SHAPES = [  # (format, N, K): the 7B and TinyLlama decode shapes, lm_head cut to 8192 rows
     (F.Q4_K, 18944, 3584), (F.Q6_K, 3584, 18944), (F.Q6_K, 8192, 3584),
     (F.Q4_0, 5632, 2048), (F.Q8_0, 2048, 5632), (F.Q4_1, 2048, 2048),
+    (F.Q4_0, 3584, 18944), (F.Q4_1, 4096, 4096),
 ]
 
 
-@pytest.mark.parametrize("kind", ["spike", "mixed", "sparse"])
+@pytest.mark.parametrize("kind", ["spike", "mixed", "sparse", "edge"])
 @pytest.mark.parametrize("dtype,N,K", SHAPES, ids=lambda v: str(v))
 def test_batch1_gguf_and_packed(dtype, N, K, kind):
     w = synth.make_weights(dtype, N, K, seed=77)
@@ -72,7 +87,7 @@ def test_batch1_gguf_and_packed(dtype, N, K, kind):
 
 @pytest.mark.parametrize("kind", ["spike", "mixed"])
 @pytest.mark.parametrize("M", [2, 3, 5, 8, 16])
-@pytest.mark.parametrize("dtype", [F.Q4_K, F.Q6_K, F.Q8_0])
+@pytest.mark.parametrize("dtype", [F.Q4_K, F.Q6_K, F.Q8_0, F.Q4_0])
 def test_small_batch_paths(dtype, M, kind):
     # cfg3-like rows (Q4_K M = 3 runs on the int8 matrix cores, M = 5..16 on
     # the one-pass fp16 MFMA kernel; M = 2 on the batch-1 kernel with two
