@@ -3,7 +3,7 @@
 //
 // Dispatch by token count (run_matmul): M = 1 runs the batch-1 GEMV kernels
 // (fq_gemvp.hip / fq_gemvt.hip over GGUF bytes or the aligned layout, the
-// row-step kernels of fq_gemv1.hip under about 8 MB of weights); M = 2..4
+// row-step kernels of fq_gemv1.hip under about 4 MB of weights); M = 2..4
 // the same batch-1 kernels with each weight unit dotted with every token;
 // Q4_K M = 4..16 the band kernel of fq_mmqs.hip; M > 32 the prefill kernel
 // of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --
@@ -971,10 +971,10 @@ int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk,
     const void* ws[3] = {wq, wk, wv};
     const int ns[3] = {Nq, Nk, Nv};
     if (M == 1) {  // the three outputs are contiguous slices of y
-        // one launch over the three matrices' GGUF rows when the batch-1
-        // kernel takes them (8 MB and more in all, or Q6_K)
-        if (packable(dtype) &&
-            (dtype == FQ_DTYPE_Q6_K || (int64_t)Nt * (K / g.be) * g.bb >= (8 << 20))) {
+        // one launch over the three matrices' GGUF rows (the five formats
+        // the batch-1 kernel reads; at every size: against three launches,
+        // TinyLlama QKV 9.4 -> 4.5 us for Q4_0, 12.3 -> 4.5 us for Q8_0)
+        if (packable(dtype)) {
             // a matrix of no rows is never read: any valid pointer stands in
             const void* any = Nq ? wq : Nk ? wk : wv;
             const int rc = packed_gemv(dtype, x, Nq ? wq : any, Nk ? wk : any, Nv ? wv : any, Nq,
@@ -1036,10 +1036,10 @@ int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const vo
     if (M == 0 || N == 0) return FQ_OK;
     if (!x || !w_gate || !w_up || !y) return FQ_ERR_NULL;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (M == 1 && packable(dtype) &&
-        (dtype == FQ_DTYPE_Q6_K || 2 * (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
-        // one launch: gate and up rows interleaved, silu(gate) * up in the
-        // epilogue, straight from the GGUF bytes
+    if (M == 1 && packable(dtype)) {
+        // one launch at every size: gate and up rows interleaved,
+        // silu(gate) * up in the epilogue, straight from the GGUF bytes
+        // (against two matmuls and the SiLU-multiply launch)
         const int rc = packed_gemv(dtype, x, w_gate, w_up, nullptr, 0, 0, 1, nullptr, 0, y, K, N,
                                    st, true);
         if (rc != FQ_ERR_SHAPE) return rc;

@@ -88,9 +88,11 @@ def test_fused_packed(name, dtype, N, K):
     ("q4_0-7b-gate-up", F.Q4_0, 18944, 3584),
     ("q6k-long-k", F.Q6_K, 700, 18944),
     ("q8_0", F.Q8_0, 1100, 4096),
+    ("tinyllama-q4_0-small", F.Q4_0, 300, 2048),
+    ("q4_1-small", F.Q4_1, 77, 512),
 ])
 def test_fused_gguf_one_launch(name, dtype, N, K):
-    # M = 1 on GGUF bytes of 8 MB and more (every Q6_K): gate and up rows
+    # M = 1 on GGUF bytes of the five batch-1 formats, any size: gate and up rows
     # interleaved in one batch-1 launch with silu(gate) * up in its epilogue;
     # the same gate and up as the two unfused GEMVs (same kernel arithmetic),
     # and deterministic
@@ -113,9 +115,12 @@ def test_fused_gguf_one_launch(name, dtype, N, K):
     ("q6_k-odd", F.Q6_K, 1024, 77, 5, 33),
     ("dual-q4_k", F.Q4_K, 3584, 2048, 2048, 0),  # matmul_transB_dual: two matrices
     ("q6_k-no-q", F.Q6_K, 1024, 0, 40, 33),
+    ("tinyllama-q4_0", F.Q4_0, 2048, 2048, 256, 256),
+    ("tinyllama-q8_0", F.Q8_0, 2048, 2048, 256, 256),
+    ("q4_1-tiny", F.Q4_1, 256, 9, 0, 5),
 ])
 def test_fused_qkv_gguf_one_launch(name, dtype, K, Nq, Nk, Nv):
-    # M = 1 on GGUF bytes of 8 MB and more in all (every Q6_K): the three
+    # M = 1 on GGUF bytes of the five batch-1 formats, any size: the three
     # matrices' rows in one batch-1 launch, y their concatenation
     ns = (Nq, Nk, Nv)
     ws = [synth.make_weights(dtype, max(n, 1), K, 50 + i) for i, n in enumerate(ns)]
@@ -149,8 +154,8 @@ def test_fused_errors():
 
 @pytest.mark.parametrize("dtype", [F.Q6_K, F.Q4_K, F.Q4_0])
 def test_fused_k0_one_token_zeros(dtype):
-    # K = 0 at M = 1: Q6_K (and 8 MB-and-more shapes) are routed to the
-    # one-launch batch-1 kernel, which never runs with no K-slices: y = 0
+    # K = 0 at M = 1: the five batch-1 formats are routed to the one-launch
+    # batch-1 kernel, which never runs with no K-slices: y = 0
     # (silu(0) * 0 for gate+up), written over a NaN-filled output
     from forge_amd import _lib
     L = _lib.lib()
