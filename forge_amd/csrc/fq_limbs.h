@@ -167,7 +167,7 @@ __device__ __forceinline__ void build_nib(uint8_t* rec, float4 xv, int i, bool l
     uint32_t v[4], pv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-        v[j] = (uint32_t)((int)__builtin_rintf(xs[j] * inv) + 0x888888) ^ 0x888888u;
+        v[j] = ((uint32_t)(int)__builtin_rintf(xs[j] * inv) + 0x888888u) ^ 0x888888u;
 #pragma unroll
     for (int j = 0; j < 4; ++j)  // lane i ^ 4 of the unit (ds_swizzle, xor mask 4)
         pv[j] = (uint32_t)__builtin_amdgcn_ds_swizzle((int)v[j], 0x101F);
