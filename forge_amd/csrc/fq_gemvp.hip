@@ -1,7 +1,7 @@
 // fq_gemvp.hip -- batch-1 GEMV over the aligned device layout (fq_pack.h).
 //
 // Every quant payload a lane needs is a 16-byte-aligned run, so weights go
-// straight from HBM to registers with coalesced global_load_dwordx4 (plus
+// straight from HBM to registers with coalesced 16-byte buffer loads (plus
 // small dense loads of the scale arrays): no LDS staging of weights.  As in
 // the row-step kernel of fq_gemv1.hip, lane l owns the same "lane units" of
 // every row (l and l + 64), its activation limbs stay in registers, and a
