@@ -155,6 +155,8 @@ struct NibRec : std::false_type {};
 template <class Fm>
 struct NibRec<Fm, std::void_t<decltype(Fm::NIB)>> : std::bool_constant<Fm::NIB> {};
 
+// Every lane of the wave runs it (the ds_swizzle exchange and the DPP group
+// reductions read the other lanes); `live` only gates the record writes.
 __device__ __forceinline__ void build_nib(uint8_t* rec, float4 xv, int i, bool live) {
     float m = fmaxf(fmaxf(__builtin_fabsf(xv.x), __builtin_fabsf(xv.y)),
                     fmaxf(__builtin_fabsf(xv.z), __builtin_fabsf(xv.w)));
