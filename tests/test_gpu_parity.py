@@ -136,6 +136,28 @@ def test_gemv_edge_shapes(dtype, N, K):
     check_shape(dtype, N, K, 1, seed=7 * N + K)
 
 
+@pytest.mark.parametrize("dtype,N,K", [
+    (F.Q4_0, 4099, 4160), (F.Q4_1, 4099, 4160), (F.Q8_0, 2051, 2080),
+    (F.Q4_K, 4097, 4352), (F.Q6_K, 1001, 4352), (F.Q4_0, 1025, 18944 + 32),
+])
+def test_batch1_ragged_k_slices(dtype, N, K):
+    # M = 1 on the K-sliced kernel (4 MB of weights and more, every Q6_K): the
+    # last K-slice of each row is partial (Q4_0 4160: 130 blocks in slices of
+    # 128, Q8_0 2080: 65 in slices of 64, Q4_K / Q6_K 4352: 68 / 68 lane units
+    # of 64), the row count odd, so the last rows' loads run past the
+    # matrix's end into the buffer bound (zeros) and the idle lanes are
+    # masked out of the row sums
+    check_shape(dtype, N, K, 1, seed=N + K, what=f"{F.fmt(dtype).name} {N}x{K} gguf")
+    if K % 256 == 0:
+        w = synth.make_weights(dtype, N, K, N + K)
+        x = synth.make_x(1, K, N + K + 1)
+        y = ops.gemv_packed(torch.from_numpy(x).to(DEV),
+                            ops.pack_weights(dev_weight(dtype, w, N, K))).cpu().numpy()
+        deq_max = float(np.max(np.abs(oracle.dequant(dtype, w, min(N, 4096), K))))
+        assert_close(y.reshape(1, -1), oracle.matmul_f64(dtype, x, w, N, K), x,
+                     np.array([deq_max]), f"{F.fmt(dtype).name} {N}x{K} aligned")
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16, 32])
 def test_small_batch_config3(M):
     # config 3: Llama-3-8B FFN up, Q4_K, speculative-verify batch sizes
