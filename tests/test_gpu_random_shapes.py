@@ -1,6 +1,8 @@
 """Seeded random shapes through ops.matmul_transB against the f64 oracle:
 every format, M from 1 to 100 (every dispatch path), N >= 16 with tails, K
-any whole number of blocks up to 8192, no bias / row bias / full bias.
+any whole number of blocks up to 8192, no bias / row bias / full bias; and
+40 shapes of 4 MB and more in the five batch-1 formats (N up to 12289, K up
+to 12288).
 Bars as in test_gpu_parity.py.
 
 The rel-L2 bar is a ratio to |y|, so it is only asserted on outputs of 16
@@ -39,7 +41,26 @@ def _cases():
     return out
 
 
-@pytest.mark.parametrize("dt,M,N,K,seed,r", _cases())
+def _large_cases():
+    # matrices of 4 MB and more: the K-sliced batch-1 kernel with 1 .. 4
+    # tokens (partial K-slices, odd row counts), the band kernel and the
+    # prefill kernel on larger row counts
+    rng = np.random.default_rng(20261202)
+    out = []
+    fives = [F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K]
+    while len(out) < 40:
+        dt = int(rng.choice(fives))
+        be = F.fmt(dt).block_elems
+        M = int(rng.choice([1, 1, 1, 2, 3, 4, 5, 8, 16, 33, 64]))
+        N = int(rng.choice([2049, 4097, 6001, 9000, 12289]))
+        K = be * int(rng.integers(max(1, 2048 // be), 12288 // be))
+        if M * N * K > 2.0e8 or N * (K // be) * F.fmt(dt).block_bytes < (4 << 20):
+            continue
+        out.append((dt, M, N, K, int(rng.integers(1 << 30)), float(rng.random())))
+    return out
+
+
+@pytest.mark.parametrize("dt,M,N,K,seed,r", _cases() + _large_cases())
 def test_random_shape(dt, M, N, K, seed, r):
     w = synth.make_weights(dt, N, K, seed=seed)
     x = synth.make_x(M, K, seed=seed + 1)
