@@ -2,8 +2,9 @@
 // argument validation, launch planning and the per-stream scratch memory.
 //
 // Dispatch by token count (run_matmul): M = 1 runs the batch-1 GEMV kernels
-// (fq_gemvp.hip / fq_gemvt.hip over GGUF bytes or the aligned layout, the
-// row-step kernels of fq_gemv1.hip under about 4 MB of weights); M = 2..4
+// (fq_gemvp.hip over GGUF bytes or the aligned layout, fq_gemvt.hip for Q8_0
+// matrices of 64k rows and more on the aligned layout, the row-step kernels
+// of fq_gemv1.hip under about 4 MB of weights); M = 2..4
 // the same batch-1 kernels with each weight unit dotted with every token;
 // Q4_K M = 4..16 the band kernel of fq_mmqs.hip; M > 32 the prefill kernel
 // of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --

@@ -47,8 +47,8 @@ const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t
 // forms, one token, no bias
 const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds_fixed,
                             int* wg, int* nl, int rows, int tokens = 1, int mode = 0);
-// batch-1 GEMV over the tiled aligned layout (fq_gemvt.hip; Q4_0, Q4_1, Q8_0
-// matrices for which packed_tiled() holds), one row per lane
+// batch-1 GEMV over the tiled aligned layout (fq_gemvt.hip; Q8_0 matrices
+// for which packed_tiled() holds), one row per lane
 struct TArgs {
     const float* x;             // [K]
     const uint8_t *w, *w2, *w3; // packed matrices (w2: up for the fused gate/up; w2, w3: K, V)
