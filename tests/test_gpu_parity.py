@@ -276,6 +276,26 @@ def test_unaligned_weight_base(dtype):
     assert np.array_equal(y0, y2)
 
 
+@pytest.mark.parametrize("dtype,N,K", [(F.Q4_0, 4608, 2048), (F.Q4_0, 300, 2048),
+                                       (F.Q4_K, 2048, 4096), (F.Q6_K, 700, 4352),
+                                       (F.Q8_0, 2100, 2048)])
+@pytest.mark.parametrize("M", [1, 2, 3, 8, 40])
+def test_activation_base_4_byte_aligned(dtype, N, K, M):
+    # x and y at a 4-byte (not 16-byte) offset, as a row slice of a larger
+    # tensor gives them: every path (batch-1, few-token, band, MMQ, prefill)
+    # reads x in 16-byte pieces, which gfx950 serves at any 4-byte alignment;
+    # the result is bit-identical to the aligned call's
+    w = synth.make_weights(dtype, N, K, seed=71)
+    x = synth.make_x(M, K, 72)
+    W = dev_weight(dtype, w, N, K)
+    xa = torch.from_numpy(x).to(DEV)
+    xo = torch.empty(M * K + 1, device=DEV)[1:].view(M, K)
+    xo.copy_(xa)
+    assert xo.data_ptr() % 16 == 4
+    np.testing.assert_array_equal(ops.matmul_transB(xo, W).cpu().numpy(),
+                                  ops.matmul_transB(xa, W).cpu().numpy())
+
+
 @pytest.mark.parametrize("dtype,M", [(F.Q4_K, 1), (F.Q4_K, 2), (F.Q4_K, 3), (F.Q6_K, 2),
                                      (F.Q8_0, 2), (F.Q4_K, 40)])
 def test_bias_modes(dtype, M):
