@@ -281,8 +281,8 @@ def test_unaligned_weight_base(dtype):
                                        (F.Q8_0, 2100, 2048)])
 @pytest.mark.parametrize("M", [1, 2, 3, 8, 40])
 def test_activation_base_4_byte_aligned(dtype, N, K, M):
-    # x and y at a 4-byte (not 16-byte) offset, as a row slice of a larger
-    # tensor gives them: every path (batch-1, few-token, band, MMQ, prefill)
+    # x at a 4-byte (not 16-byte) offset, as a slice of a larger tensor can
+    # place it: every path (batch-1, few-token, band, MMQ, prefill)
     # reads x in 16-byte pieces, which gfx950 serves at any 4-byte alignment;
     # the result is bit-identical to the aligned call's
     w = synth.make_weights(dtype, N, K, seed=71)
