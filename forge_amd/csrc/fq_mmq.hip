@@ -602,18 +602,34 @@ __global__ __launch_bounds__(64 * NWN * NWM) void mmq_kernel(MmqArgs a) {
 // y = sum over splits of the partial slabs, in split order, plus the bias.
 // Four consecutive outputs per thread (16-byte loads and stores), the same
 // split order: bit-identical to reduce_kernel.  Needs M N and N multiples of
-// 4 and a 16-byte aligned y.
+// 4 and a 16-byte aligned y.  S > 0: the split count at compile time, so all
+// S slab loads of a thread are in flight at once (a runtime count loop waits
+// for each load before issuing the next); S = 0: any count.
+template <int S>
 __global__ __launch_bounds__(256) void reduce4_kernel(MmqArgs a, int splits) {
     const size_t total = (size_t)a.M * a.N, t4 = total / 4;
     const float4* part = reinterpret_cast<const float4*>(a.part);
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < t4; i += (size_t)gridDim.x * 256) {
         float4 v = part[i];
-        for (int z = 1; z < splits; ++z) {
-            const float4 u = part[(size_t)z * t4 + i];
-            v.x += u.x;
-            v.y += u.y;
-            v.z += u.z;
-            v.w += u.w;
+        if constexpr (S > 0) {
+            float4 u[S];
+#pragma unroll
+            for (int z = 1; z < S; ++z) u[z] = part[(size_t)z * t4 + i];
+#pragma unroll
+            for (int z = 1; z < S; ++z) {
+                v.x += u[z].x;
+                v.y += u[z].y;
+                v.z += u[z].z;
+                v.w += u[z].w;
+            }
+        } else {
+            for (int z = 1; z < splits; ++z) {
+                const float4 u = part[(size_t)z * t4 + i];
+                v.x += u.x;
+                v.y += u.y;
+                v.z += u.z;
+                v.w += u.w;
+            }
         }
         const int n = (int)((4 * i) % a.N);
         if (a.bias_mode == 1) {
@@ -688,7 +704,15 @@ hipError_t launch_reduce(const MmqArgs& a, int splits, hipStream_t st) {
         (reinterpret_cast<uintptr_t>(a.part) & 15) == 0) {
         const size_t t4 = total / 4;
         const int grid = (int)((t4 + 255) / 256 < 4096 ? (t4 + 255) / 256 : 4096);
-        hipLaunchKernelGGL(reduce4_kernel, dim3(grid), dim3(256), 0, st, a, splits);
+        switch (splits) {
+            case 2: hipLaunchKernelGGL(reduce4_kernel<2>, dim3(grid), dim3(256), 0, st, a, splits); break;
+            case 3: hipLaunchKernelGGL(reduce4_kernel<3>, dim3(grid), dim3(256), 0, st, a, splits); break;
+            case 4: hipLaunchKernelGGL(reduce4_kernel<4>, dim3(grid), dim3(256), 0, st, a, splits); break;
+            case 5: hipLaunchKernelGGL(reduce4_kernel<5>, dim3(grid), dim3(256), 0, st, a, splits); break;
+            case 6: hipLaunchKernelGGL(reduce4_kernel<6>, dim3(grid), dim3(256), 0, st, a, splits); break;
+            case 8: hipLaunchKernelGGL(reduce4_kernel<8>, dim3(grid), dim3(256), 0, st, a, splits); break;
+            default: hipLaunchKernelGGL(reduce4_kernel<0>, dim3(grid), dim3(256), 0, st, a, splits);
+        }
         return hipGetLastError();
     }
     const int grid = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
