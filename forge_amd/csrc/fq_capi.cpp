@@ -325,7 +325,7 @@ int noalloc_workspace(int dev, uint8_t** out) {
 int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
                 const void* w3_packed, int n1, int n2, int mode, const float* bias,
                 int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf, int M = 1,
-                bool bias_full = false);
+                bool bias_full = false, uint8_t* fixed = nullptr, size_t fixed_cap = 0);
 
 int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias, int bias_mode,
                int64_t bias_len, float* y, int M, int K, int N, hipStream_t st, uint8_t* fixed,
@@ -367,11 +367,12 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     if (M >= 2 && M <= 4 && K > 0 && packable(dtype) &&
         (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
         // two to four tokens: the same kernel dots each weight unit it reads
-        // with every token's limbs (FQ_ERR_SHAPE: the tokens' records do not
-        // fit LDS)
+        // with every token's limbs, K split into slabs where the tokens'
+        // records of a whole row do not fit LDS (FQ_ERR_SHAPE: no split fits,
+        // or the slabs need workspace the call cannot have)
         const int rc = packed_gemv(dtype, x, w, nullptr, nullptr, 0, 0, 0,
                                    bias_mode ? bias : nullptr, bias_mode == 2 ? N : bias_len, y,
-                                   K, N, st, true, M, bias_mode == 2);
+                                   K, N, st, true, M, bias_mode == 2, fixed, fixed_cap);
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
@@ -701,7 +702,7 @@ int run_gemvt(uint32_t dtype, const float* x, const void* w, const void* w2, con
 int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void* w2_packed,
                 const void* w3_packed, int n1, int n2, int mode, const float* bias,
                 int64_t bias_len, float* y, int K, int N, hipStream_t st, bool gguf, int M,
-                bool bias_full) {
+                bool bias_full, uint8_t* fixed, size_t fixed_cap) {
     Geometry g;
     if (!geometry(dtype, g) || !packable(dtype)) return FQ_ERR_DTYPE;
     if (N < 0 || K < 0 || K % (gguf ? g.be : 256) != 0) return FQ_ERR_SHAPE;
@@ -760,6 +761,42 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
                                    M, mode)
              : fq::gemvp_kernel_fn((int)dtype, units, records, bias != nullptr, &lds, &wg, &nl,
                                    mode);
+    // K split over blockIdx.y for several tokens whose records of a whole row
+    // do not fit LDS (K = 18944: 2 x 85 KB): each work-group stages only the
+    // records of its own K-slices and writes partial sums, [splits][M][N],
+    // which the slab sum adds with the bias (the fewest splits that fit)
+    int splits = 1, spl = 0;
+    if (gguf && fn && M >= 2 && lds + 64 * 4 * M + 256 > lds_cap) {
+        fn = fq::gemvg_kernel_fn((int)dtype, units, records, false, &lds, &wg, &nl, NV, M, mode);
+        if (!fn) return FQ_ERR_SHAPE;
+        const size_t rb = (size_t)fq::gemvp_record_bytes();
+        const size_t wbufs = lds - (size_t)M * records * rb;
+        const int nrec = records / units, ns_all = (units + 64 * nl - 1) / (64 * nl);
+        for (int s = 2; s <= 8 && !spl; ++s) {
+            const int sp = (ns_all + s - 1) / s;
+            const size_t l = (size_t)M * std::min(units, sp * 64 * nl) * nrec * rb + wbufs;
+            if (l + 64 * 4 * M * (size_t)sp + 256 <= lds_cap) {
+                spl = sp;
+                splits = (ns_all + sp - 1) / sp;
+                lds = l;
+            }
+        }
+        if (!spl) return FQ_ERR_SHAPE;
+    }
+    std::unique_ptr<StreamScratch::Lease> lease;
+    uint8_t* slab = fixed;
+    if (splits > 1) {
+        const size_t need = (size_t)splits * M * NV * sizeof(float);
+        if (fixed) {
+            if (need > fixed_cap) return FQ_ERR_SHAPE;
+        } else {
+            lease.reset(new StreamScratch::Lease(stream_scratch(dev, st, 0)));
+            const int rc = lease->get(need, st, &slab);
+            // under graph capture without a reserved workspace: another kernel
+            if (rc == FQ_ERR_WORKSPACE) return FQ_ERR_SHAPE;
+            if (rc != FQ_OK) return rc;
+        }
+    }
     if (gguf) {
         // M tokens' partial sums per row and K-slice
         // (256 bytes left for the kernel's static LDS: its step counter)
@@ -776,8 +813,8 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     // one work-group per resident slot, each owning a contiguous row range
     // with at least one row per wave, and whose row x K-slice partial sums fit
     // its LDS buffer (slices of 64 lane units)
-    const long ns = (units + 64 * nl - 1) / (64 * nl);
-    long G = (long)di.cus * per_cu;
+    const long ns = spl ? spl : (units + 64 * nl - 1) / (64 * nl);
+    long G = ((long)di.cus * per_cu + splits - 1) / splits;
     G = std::max(1L, std::min<long>(G, ((long)NV + wpb - 1) / wpb));
     auto max_rows = [&](long g) { return dual ? 2 * ((N + g - 1) / g) : (NV + g - 1) / g; };
     G = std::max<long>(G, ((long)NV * ns + pcap - 1) / pcap);
@@ -800,7 +837,24 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
     a.U = units;
     a.Uc = records;
     a.row_bytes = gguf ? (K / g.be) * g.bb : (int)fq::packed_row_bytes((int)dtype, K);
-    e = fq::launch_raw(fn, a, (int)G, wg, lds, st);
+    if (splits > 1) {
+        a.part = reinterpret_cast<float*>(slab);
+        a.spl = spl;
+        a.bias = nullptr;
+        a.bias_len = 0;
+        a.bias_mode = 0;
+    }
+    e = fq::launch_raw(fn, a, (int)G, wg, lds, st, splits);
+    if (e != hipSuccess || splits == 1) return e == hipSuccess ? FQ_OK : hip_fail(e);
+    fq::MmqArgs r{};
+    r.part = a.part;
+    r.y = y;
+    r.bias = bias;
+    r.bias_len = bias ? bias_len : 0;
+    r.bias_mode = bias ? (bias_full ? 2 : 1) : 0;
+    r.M = M;
+    r.N = NV;
+    e = fq::launch_reduce(r, splits, st);
     return e == hipSuccess ? FQ_OK : hip_fail(e);
 }
 
@@ -1081,6 +1135,8 @@ int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
             need0 = std::max(need0, plan_mmq(m, K_max, n, di.cus).total);
             if (m >= 4 && m <= 16 && Kp > 0) need0 = std::max(need0, mmqs_need(m, Kp, n, di.cus));
             if (m > 32 && Kp > 0) need0 = std::max(need0, plan_mmqp(m, Kp, n, di.cus, true).total);
+            // the batch-1 kernel's K-split slabs for 2..4 tokens (at most 8)
+            if (m <= 4) need0 = std::max(need0, (size_t)8 * m * n * sizeof(float));
         }
     }
     const size_t need1 = 2 * (size_t)M_max * N_max * sizeof(float);

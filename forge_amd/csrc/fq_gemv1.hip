@@ -454,10 +454,10 @@ const void* gemv1r_kernel_fn(int dtype, int U, int row_bytes, bool bias, int* np
 }
 
 hipError_t launch_raw(const void* fn, const GemvArgs& a, int grid, int wg, size_t lds,
-                      hipStream_t st) {
+                      hipStream_t st, int grid_y) {
     GemvArgs args = a;
     void* params[] = {&args};
-    return hipLaunchKernel(fn, dim3(grid), dim3(wg), params, lds, st);
+    return hipLaunchKernel(fn, dim3(grid, grid_y), dim3(wg), params, lds, st);
 }
 
 hipError_t launch_gemv1(int dtype, const GemvArgs& a, int grid, int wg, hipStream_t st) {

@@ -450,11 +450,18 @@ __device__ __forceinline__ Step step_of(int f, int rows, float inv_rows) {
 // the next loads are issued into the freed registers, then each lane reads
 // its unit from the buffer.  A wave's LDS accesses execute in order, so no
 // barrier separates the writes from the reads.
+// A work-group's K range: its first K-slice sl0 (steps count slices from
+// there), its lane units Ul and each token's records Rl in LDS (the whole row
+// unless the host splits K over blockIdx.y).
+struct KRange {
+    int sl0, Ul, Rl;
+};
+
 // Limb reloads: RL 0 never (rows of one K-slice: loaded before the loop),
 // 1 when the step's slice differs from the wave's last, 2 every step.
 template <int F, int NL, int MODE, int GP, int NT, int RL>
 __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& st, int& nxt,
-                                      const Claims& cl, const GemvArgs& a,
+                                      const Claims& cl, const GemvArgs& a, const KRange& kr,
                                       Limbs (&L)[NT][NL][Pk<F>::NREC], const uint8_t* lds,
                                       uint8_t* wbuf, float* part, int lo, int lane, int& cur_s) {
     __builtin_amdgcn_sched_barrier(0);
@@ -464,10 +471,10 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& 
     if (RL == 2 || (RL == 1 && cp.f >= 0 && cp.s != cur_s)) {  // wave-uniform
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-            load_slice_limbs<F, NL>(L[t], lds + (size_t)t * a.Uc * RECB, cp.s, a.U, lane);
+            load_slice_limbs<F, NL>(L[t], lds + (size_t)t * kr.Rl * RECB, cp.s, kr.Ul, lane);
         cur_s = cp.s;
     }
-    const int v0 = cp.s * 64 * NL;
+    const int v0 = (kr.sl0 + cp.s) * 64 * NL;  // the step's first lane unit in the row
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -481,17 +488,17 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& 
                 acc[t] += v < a.U ? d : 0.0f;
             }
         }
-        pload<F, NL, MODE, GP>(f, a, st.s, st.r, lo, lane);
+        pload<F, NL, MODE, GP>(f, a, kr.sl0 + st.s, st.r, lo, lane);
     } else {
 #pragma unroll
         for (int i = 0; i < GP; ++i) reinterpret_cast<uint4*>(wbuf)[lane + 64 * i] = f[0].v[i];
-        const int shift =
-            (int)(reinterpret_cast<uintptr_t>(gslice<F, NL, MODE>(a, cp.s, cp.r, lo)) & 15);
+        const int shift = (int)(reinterpret_cast<uintptr_t>(
+                                    gslice<F, NL, MODE>(a, kr.sl0 + cp.s, cp.r, lo)) & 15);
         typename Pk<F>::Raw raw[NL];
 #pragma unroll
         for (int c = 0; c < NL; ++c)
             raw[c] = Gk<F>::read(wbuf + shift, min(v0 + lane + 64 * c, a.U - 1) - v0);
-        pload<F, NL, MODE, GP>(f, a, st.s, st.r, lo, lane);
+        pload<F, NL, MODE, GP>(f, a, kr.sl0 + st.s, st.r, lo, lane);
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
             const int v = v0 + lane + 64 * c;
@@ -518,7 +525,10 @@ __device__ __forceinline__ void pstep(typename RegSel<F, GP>::T (&f)[NL], Step& 
 // (sized by the host).  NT tokens (MODE ONE, GGUF rows): every weight unit
 // read and decoded once is dotted with each token's limbs; token t's records
 // follow token t - 1's, and y, the partial sums and a full bias
-// (a.bias_mode 2) are token-major.
+// (a.bias_mode 2) are token-major.  Where the tokens' records of a whole row
+// do not fit LDS the host splits K: work-group (g, y) stages the records of
+// K-slices y a.spl .. (y + 1) a.spl - 1 only and writes its row sums, without
+// the bias, to slab y of a.part for the slab sum.
 template <int F, int NL, int D, bool BIAS, int WG, int MODE = ONE, int GP = 0, int NT = 1,
           bool OS = false>
 __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
@@ -532,13 +542,24 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     if constexpr (GP == 0) {
         __shared__ float part_s[YBUF];
         part = part_s;
-    } else {
-        wbuf = lds + (size_t)NT * a.Uc * RECB + (threadIdx.x >> 6) * (GP * 1024);
-        part = reinterpret_cast<float*>(lds + (size_t)NT * a.Uc * RECB + W * GP * 1024);
     }
     using P = Pk<F>;
+    // K split over blockIdx.y (several tokens only; a.spl slices per split,
+    // 0: unsplit): this work-group's slices, lane units and records per token
+    const bool split = NT > 1 && a.spl > 0;
+    const int ns_all = (a.U + 64 * NL - 1) / (64 * NL);
+    KRange kr{0, a.U, a.Uc};
+    if (split) {
+        kr.sl0 = (int)blockIdx.y * a.spl;
+        kr.Ul = min(a.U - kr.sl0 * 64 * NL, a.spl * 64 * NL);
+        kr.Rl = kr.Ul * P::NREC;
+    }
+    if constexpr (GP > 0) {
+        wbuf = lds + (size_t)NT * kr.Rl * RECB + (threadIdx.x >> 6) * (GP * 1024);
+        part = reinterpret_cast<float*>(lds + (size_t)NT * kr.Rl * RECB + W * GP * 1024);
+    }
     const int lane = threadIdx.x & 63;
-    const int ns = (a.U + 64 * NL - 1) / (64 * NL);
+    const int ns = split ? min(ns_all - kr.sl0, a.spl) : ns_all;
     const int G = gridDim.x, g = blockIdx.x;
     // the host sizes the grid so (hi - lo) * ns <= YBUF
     const int lo = DUAL ? 2 * (int)((int64_t)(a.N / 2) * g / G) : (int)((int64_t)a.N * g / G);
@@ -563,13 +584,15 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     typename RegSel<F, GP>::T f[D][NL];
     {
         XStage<P, WG> xs;
-        stage_load<P, WG>(xs, a.x, NT * a.Uc, 0, NT > 1 ? a.Uc : 0, a.K);
-        pload<F, NL, MODE, GP>(f[0], a, st[0].s, st[0].r, lo, lane);
-        stage_build<P, WG, false>(lds, xs, a.x, NT * a.Uc, 0, NT > 1 ? a.Uc : 0, a.K);
+        const int r0 = kr.sl0 * 64 * NL * P::NREC;  // the range's first record
+        stage_load<P, WG>(xs, a.x, NT * kr.Rl, r0, NT > 1 ? kr.Rl : 0, a.K);
+        pload<F, NL, MODE, GP>(f[0], a, kr.sl0 + st[0].s, st[0].r, lo, lane);
+        stage_build<P, WG, false>(lds, xs, a.x, NT * kr.Rl, r0, NT > 1 ? kr.Rl : 0, a.K);
     }
     lds_barrier();  // the weight loads stay in flight
 #pragma unroll
-    for (int j = 1; j < D; ++j) pload<F, NL, MODE, GP>(f[j], a, st[j].s, st[j].r, lo, lane);
+    for (int j = 1; j < D; ++j)
+        pload<F, NL, MODE, GP>(f[j], a, kr.sl0 + st[j].s, st[j].r, lo, lane);
     Limbs L[NT][NL][P::NREC];
     int cur_s = -1;
     // every iteration runs all D slots, each issuing its loads, so the number
@@ -586,13 +609,13 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
     if constexpr (RL == 0) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-            load_slice_limbs<F, NL>(L[t], lds + (size_t)t * a.Uc * RECB, 0, a.U, lane);
+            load_slice_limbs<F, NL>(L[t], lds + (size_t)t * kr.Rl * RECB, 0, kr.Ul, lane);
     }
     while (st[0].f >= 0) {
 #pragma unroll
         for (int j = 0; j < D; ++j)
-            pstep<F, NL, MODE, GP, NT, RL>(f[j], st[j], nxt, cl, a, L, lds, wbuf, part, lo, lane,
-                                           cur_s);
+            pstep<F, NL, MODE, GP, NT, RL>(f[j], st[j], nxt, cl, a, kr, L, lds, wbuf, part, lo,
+                                           lane, cur_s);
     }
     __syncthreads();
     if constexpr (DUAL) {
@@ -606,7 +629,10 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
         }
     } else {
         // the bias is added to the finished row sum, as apply_bias adds it to
-        // the finished product (matmul.cpp:1005-1049)
+        // the finished product (matmul.cpp:1005-1049); a K split writes its
+        // slab of partial sums (split-major, then token-major) and the slab
+        // sum adds the bias
+        float* out = split ? a.part + (size_t)blockIdx.y * NT * a.N : a.y;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const float* bias = a.bias + (a.bias_mode == 2 ? (size_t)t * a.N : 0);
@@ -614,7 +640,7 @@ __global__ __launch_bounds__(WG) void gemvp_kernel(GemvArgs a) {
                 float v = part[t * cl.total + r];
                 for (int s = 1; s < ns; ++s) v += part[t * cl.total + s * rows + r];
                 if constexpr (BIAS) v += lo + r < a.bias_len ? bias[lo + r] : 0.0f;
-                a.y[(size_t)t * a.N + lo + r] = v;
+                out[(size_t)t * a.N + lo + r] = v;
             }
         }
     }
@@ -825,6 +851,8 @@ const void* gfn_mode(int mode, int units, int* gp) {
 }  // namespace
 
 // Lane units per row and activation records for a packed GEMV of length K.
+int gemvp_record_bytes() { return RECB; }
+
 void gemvp_geometry(int dtype, int K, int* units, int* records) {
     if (dtype == Q6_K || dtype == Q4_K) {
         *units = K / 64;

@@ -22,6 +22,8 @@ struct GemvArgs {
     int Uc;               // kernel-specific count: batch-1 activation records per
                           // token (gemvp), units or steps per chunk (the others)
     int row_bytes;
+    float* part;          // gemvp K split: [splits][M][N] partial sums
+    int spl;              // gemvp K split: K-slices per split (0: unsplit)
 };
 
 // batch-1 persistent kernel (fq_gemv1.hip)
@@ -34,9 +36,10 @@ hipError_t launch_gemv1(int dtype, const GemvArgs& a, int grid, int wg, hipStrea
 const void* gemv1r_kernel_fn(int dtype, int U, int row_bytes, bool bias, int* npr_out,
                              size_t* lds_out, int* wg_out, int nt = 1);
 hipError_t launch_raw(const void* fn, const GemvArgs& a, int grid, int wg, size_t lds,
-                      hipStream_t st);
+                      hipStream_t st, int grid_y = 1);
 // packed-layout batch-1 kernels (fq_gemvp.hip)
 void gemvp_geometry(int dtype, int K, int* units, int* records);
+int gemvp_record_bytes();  // LDS bytes of one activation record
 // nl: lane units per lane and step (K-slices are 64 nl units)
 const void* gemvp_kernel_fn(int dtype, int units, int records, bool bias, size_t* lds, int* wg,
                             int* nl, int mode = 0);

@@ -52,6 +52,9 @@ def test_noalloc_every_m_path():
     for M in (1, 2, 3, 4):
         _pair(F.Q6_K, M, 2048, 3000, 70 + M, bias=M == 3)
     _pair(F.Q4_K, 8, 4096, 4096, 80)
+    # the batch-1 kernel with K split into slabs (two, then four tokens)
+    _pair(F.Q6_K, 2, 18944, 3000, 90, bias=True)
+    _pair(F.Q4_0, 4, 18944, 1500, 91)
 
 
 def test_noalloc_prefill_and_limit():
