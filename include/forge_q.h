@@ -25,7 +25,10 @@
  *  - Return value: FQ_OK or one of the FQ_ERR_* codes below; the reference
  *    throws std::runtime_error for the same conditions (matmul.cpp:1135-1146,
  *    1163-1165, 1315) or launches unchecked.
- *  - Calls on the M > 1 matrix-core path and the GGUF fused ops use a
+ *  - Calls on the M > 1 matrix-core path, the batch-1 kernel at 2..4 tokens
+ *    with K split into slabs (long rows, e.g. K = 18944; under graph capture
+ *    without a reserved workspace such a call takes another kernel instead)
+ *    and the GGUF fused ops use a
  *    library-owned per-device, per-stream workspace (token operands, split-K
  *    partial slabs, intermediate rows; for Q6_K prefill, M > 32, the rows
  *    rewritten into 36-byte blocks of int8 codes: N * K * 9 / 8 bytes).  It grows on demand inside a call
@@ -208,7 +211,8 @@ int fq_ffn_down_residual_packed(uint32_t dtype, const float* x, const void* w_pa
                                 const float* residual, float* y, int K, int N, void* stream);
 
 /* fq_matmul_transB without any allocation: the same results (the same
- * kernels and launch plan), with the M > 1 matrix-core path's workspace taken
+ * kernels and launch plan), with the M > 1 workspace (matrix-core path,
+ * split-K slabs of the batch-1 kernel at 2..4 tokens) taken
  * from a fixed 64 MiB device array that the library holds on every GPU it
  * runs on, instead of the per-stream workspace.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP-graph
