@@ -109,6 +109,25 @@ def test_fused_gguf_one_launch(name, dtype, N, K):
     assert torch.equal(y, ops.ffn_up_fused(xd, Wg, Wu)), "fused GGUF GEMV is not deterministic"
 
 
+def test_fused_q4k_unaligned_base():
+    # the fused forms on Q4_K GGUF rows with one matrix at a 2-byte offset
+    # from an aligned allocation: each matrix's K-slices are staged from the
+    # aligned superset of their bytes, so the outputs are bit-identical to
+    # the all-aligned call's
+    N, K = 2048, 3584
+    wg, wu = make(F.Q4_K, N, K, 61)
+    wv = synth.make_weights(F.Q4_K, 512, K, 63)
+    x = synth.make_x(1, K, seed=64)
+    xd = torch.from_numpy(x).cuda()
+    A = [dev_weight(F.Q4_K, w, n, K) for w, n in ((wg, N), (wu, N), (wv, 512))]
+    B = [dev_weight(F.Q4_K, wg, N, K), dev_weight(F.Q4_K, wu, N, K, offset=2),
+         dev_weight(F.Q4_K, wv, 512, K)]
+    y = ops.ffn_up_fused(xd, A[0], A[1])
+    check(y.cpu().numpy(), F.Q4_K, x, wg, wu, N, K, "q4_k fused")
+    assert torch.equal(y, ops.ffn_up_fused(xd, B[0], B[1]))
+    assert torch.equal(ops.fused_qkv(xd, *A), ops.fused_qkv(xd, *B))
+
+
 @pytest.mark.parametrize("name,dtype,K,Nq,Nk,Nv", [
     ("qwen7b-q4_k", F.Q4_K, 3584, 3584, 512, 512),
     ("q8_0", F.Q8_0, 4096, 2048, 512, 512),

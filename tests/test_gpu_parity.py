@@ -277,6 +277,26 @@ def test_unaligned_weight_base(dtype):
     assert np.array_equal(y0, y2)
 
 
+@pytest.mark.parametrize("N,K", [(4096, 3584), (1100, 18944)])
+def test_q4k_gguf_unaligned_base(N, K):
+    # batch 1 on Q4_K GGUF rows at 16-byte aligned and 2-byte offset bases
+    # (K = 3584 is one partial K-slice, 18944 ends in one): each K-slice is
+    # staged through LDS from the aligned superset of its bytes, so the base's
+    # alignment changes only the staging offset and the outputs are
+    # bit-identical
+    w = synth.make_weights(F.Q4_K, N, K, seed=N + 5)
+    x = synth.make_x(1, K, N + 6)
+    b = torch.linspace(-1, 1, N)
+    ys = [run(F.Q4_K, w, x, N, K, offset=o, bias=b) for o in (0, 16, 2)]
+    np.testing.assert_array_equal(ys[0], ys[1])
+    np.testing.assert_array_equal(ys[0], ys[2])
+    y = run(F.Q4_K, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(F.Q4_K, w, N, K))))
+    assert_close(y, oracle.matmul_f64(F.Q4_K, x, w, N, K), x, np.array([deq_max]),
+                 f"Q4_K {N}x{K}")
+    np.testing.assert_allclose(ys[0], y + b.numpy(), rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("dtype,N,K", [(F.Q4_0, 4608, 2048), (F.Q4_0, 300, 2048),
                                        (F.Q4_K, 2048, 4096), (F.Q6_K, 700, 4352),
                                        (F.Q8_0, 2100, 2048)])
