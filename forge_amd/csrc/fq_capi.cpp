@@ -364,6 +364,25 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
+    if (dtype == FQ_DTYPE_Q6_K && (M == 4 || M == 5) && K > 0 &&
+        (int64_t)N * (K / g.be) * g.bb >= (24 << 20)) {
+        // four or five Q6_K tokens on 24 MB and more: three on the batch-1
+        // kernel, then the rest (its four-token form spills, and the MFMA
+        // path takes twice the three-token time: M = 4 / 5 at 3584 x 18944
+        // 59.0 / 59.1 -> 45.6 / 53.6 us, 14336 x 4096 33.8 / 41.2 -> 29.9 /
+        // 32.9, 152064 x 3584 257 -> 196 / 212; at 4096 x 4096 (14 MB) the
+        // MFMA path is faster, 13.4 against 16.7 us at M = 4)
+        for (int t0 = 0; t0 < M; t0 += 3) {
+            const int m = std::min(3, M - t0);
+            const int rc = run_matmul(dtype, x + (size_t)t0 * K, w,
+                                      bias_mode == 2 ? bias + (size_t)t0 * N : bias, bias_mode,
+                                      bias_mode == 2 ? (int64_t)m * N : bias_len,
+                                      y + (size_t)t0 * N, m, K, N, st, fixed, fixed_cap);
+            if (rc != FQ_OK) return rc;
+        }
+        return FQ_OK;
+    }
+
     if (M >= 2 && M <= 4 && K > 0 && packable(dtype) &&
         (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
         // two to four tokens: the same kernel dots each weight unit it reads

@@ -277,6 +277,28 @@ def test_unaligned_weight_base(dtype):
     assert np.array_equal(y0, y2)
 
 
+@pytest.mark.parametrize("M", [4, 5])
+def test_q6k_four_five_tokens_in_groups(M):
+    # four or five Q6_K tokens on 24 MB and more run as three tokens on the
+    # batch-1 kernel, then the rest: the rows equal those separate calls bit
+    # for bit, with each bias form
+    N, K = 2000, 18944
+    w = synth.make_weights(F.Q6_K, N, K, seed=M + 80)
+    x = synth.make_x(M, K, M + 81)
+    y = run(F.Q6_K, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(F.Q6_K, w, N, K))))
+    assert_close(y, oracle.matmul_f64(F.Q6_K, x, w, N, K), x, np.array([deq_max]),
+                 f"Q6_K M={M} {N}x{K}")
+    np.testing.assert_array_equal(y[:3], run(F.Q6_K, w, x[:3], N, K))
+    np.testing.assert_array_equal(y[3:], run(F.Q6_K, w, x[3:], N, K))
+    b1 = torch.linspace(-1, 1, N)
+    np.testing.assert_allclose(run(F.Q6_K, w, x, N, K, bias=b1), y + b1.numpy(), rtol=1e-6,
+                               atol=1e-6)
+    b2 = torch.randn(M, N)
+    np.testing.assert_allclose(run(F.Q6_K, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
+                               atol=1e-6)
+
+
 @pytest.mark.parametrize("N,K", [(4096, 3584), (1100, 18944)])
 def test_q4k_gguf_unaligned_base(N, K):
     # batch 1 on Q4_K GGUF rows at 16-byte aligned and 2-byte offset bases
