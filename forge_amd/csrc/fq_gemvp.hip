@@ -766,10 +766,22 @@ const void* gfn(int units, bool bias, bool deep, int* gp, int* nl) {
 // need up to 256, so 512 threads (three and four tokens: one lane unit).
 // Three tokens against the other kernels: cfg3 Q4_K 16.3 against 20.7 us,
 // Q6_K lm_head 128 against 227, Q8_0 14336 x 4096 19.3 against 22.7; four
-// tokens (Q4_0, Q4_1, Q8_0): Q8_0 22.7 against 26.4.
-template <int NL, int NT>
+// tokens (Q4_0, Q4_1, Q8_0): Q8_0 22.7 against 26.4.  Q4_0 and Q4_1 with one
+// lane unit per lane (nibble records: fewer live registers) and Q8_0 with
+// three tokens fit 1024 threads: 3584 x 18944 Q4_0 M = 2 / 3 / 4 20.2 /
+// 29.4 / 37.4 -> 19.1 / 26.2 / 30.8 us, 14336 x 4096 Q8_0 M = 3 19.0 ->
+// 16.8 (Q8_0 M = 4 22.3 -> 34.2, Q4_K and Q6_K three to six times slower:
+// they spill).
+constexpr int wg_tok(int f, int nl, int nt) {
+    return nl == 2                           ? 512
+           : f == Q4_0 || f == Q4_1          ? 1024
+           : f == Q8_0 && nt == 3            ? 1024
+           : nt > 2                          ? 512
+                                             : 768;
+}
+template <int F, int NL, int NT>
 constexpr int wg_t() {
-    return NL == 2 || NT > 2 ? 512 : 768;
+    return wg_tok(F, NL, NT);
 }
 
 template <int F, int NL, int GP, int NT>
@@ -777,7 +789,7 @@ const void* gfn_t(bool bias, bool os) {
     if constexpr (GP > max_pieces<F>() * NL) {
         return nullptr;
     } else {
-        constexpr int WG = wg_t<NL, NT>();
+        constexpr int WG = wg_t<F, NL, NT>();
         return bias ? kfn<F, NL, DP, true, WG, ONE, GP, NT>(os)
                     : kfn<F, NL, DP, false, WG, ONE, GP, NT>(os);
     }
@@ -913,7 +925,7 @@ const void* gemvg_kernel_fn(int dtype, int units, int records, bool bias, size_t
             case Q4_K: fn = gfn_tokens<Q4_K>(tokens, units, bias, &gp, nl); break;
             case Q6_K: fn = gfn_tokens<Q6_K>(tokens, units, bias, &gp, nl); break;
         }
-        *wg = *nl == 2 ? 512 : tokens > 2 ? 512 : 768;
+        *wg = wg_tok(dtype, *nl, tokens);
         *lds_fixed = (size_t)tokens * records * RECB + (size_t)(*wg / 64) * gp * 1024;
         return fn;
     }
