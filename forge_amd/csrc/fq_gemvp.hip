@@ -795,6 +795,20 @@ const void* gfn_t(bool bias, bool os) {
     }
 }
 
+// one lane unit per lane
+template <int F, int NT>
+const void* gfnt_one(int units, bool bias, int* gp) {
+    const bool os = units <= 64;
+    *gp = slice_pieces<F>(units < 64 ? units : 64);
+    switch (*gp) {
+        case 1: return gfn_t<F, 1, 1, NT>(bias, os);
+        case 2: return gfn_t<F, 1, 2, NT>(bias, os);
+        case 3: return gfn_t<F, 1, 3, NT>(bias, os);
+        case 4: return gfn_t<F, 1, 4, NT>(bias, os);
+        default: return nullptr;
+    }
+}
+
 template <int F, int NT>
 const void* gfnt(int units, bool bias, int* gp, int* nl) {
     *nl = lane_units<F>(units);
@@ -807,17 +821,15 @@ const void* gfnt(int units, bool bias, int* gp, int* nl) {
                     case 2: return gfn_t<F, 2, 2, NT>(bias, os);
                     case 3: return gfn_t<F, 2, 3, NT>(bias, os);
                 }
+                return nullptr;
+            } else {
+                // three and four tokens: one lane unit per lane
+                *nl = 1;
+                return gfnt_one<F, NT>(units, bias, gp);
             }
-            return nullptr;
         }
     }
-    switch (*gp) {
-        case 1: return gfn_t<F, 1, 1, NT>(bias, os);
-        case 2: return gfn_t<F, 1, 2, NT>(bias, os);
-        case 3: return gfn_t<F, 1, 3, NT>(bias, os);
-        case 4: return gfn_t<F, 1, 4, NT>(bias, os);
-        default: return nullptr;
-    }
+    return gfnt_one<F, NT>(units, bias, gp);
 }
 
 template <int F>

@@ -171,10 +171,12 @@ def test_few_tokens_batch1_kernel(dtype, N, K, M):
     # M = 2 .. 4 on weights of 8 MB and more (every Q6_K; below that M = 1 and
     # M > 1 take other kernels): the batch-1 kernel
     # dots each weight unit with every token's limbs (Q4_K and Q6_K: up to
-    # three tokens; Q4_0 and Q4_1 rows of two lane units: two).  Each token's
-    # arithmetic and summation order are the batch-1 kernel's, so where the
-    # call takes that kernel token t's row equals the M = 1 result bit for
-    # bit; the oracle pins every case.  Every bias form is added after the
+    # three tokens).  Q4_0 and Q4_1 rows of 65-192 blocks take two lane units
+    # per lane at one and two tokens, one at three and four (so those rows'
+    # K-slices, and their summation order, differ from the M = 1 call's).
+    # Otherwise each token's arithmetic and summation order are the batch-1
+    # kernel's, so token t's row equals the M = 1 result bit for bit; the
+    # oracle pins every case.  Every bias form is added after the
     # sum.  At K = 18944 the tokens' records need more LDS than there is: the
     # kernel splits K and a second pass adds the slabs, in another order than
     # the M = 1 sum.
