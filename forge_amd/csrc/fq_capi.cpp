@@ -6,7 +6,8 @@
 // matrices of 64k rows and more on the aligned layout, the row-step kernels
 // of fq_gemv1.hip under about 4 MB of weights); M = 2..4
 // the same batch-1 kernels with each weight unit dotted with every token;
-// Q4_K M = 4..16 the band kernel of fq_mmqs.hip; M > 32 the prefill kernel
+// Q4_K and Q4_0 M = 4..16 the band kernel of fq_mmqs.hip (Q6_K M = 4, 5 from
+// 24 MB: three tokens, then the rest); M > 32 the prefill kernel
 // of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --
 // the reference's batched GEMV (1 < M <= 32) and dequant + GEMM prefill
 // (M > 32), matmul.cpp:1150-1286 -- the int8 and fp16 MFMA kernels of
@@ -383,7 +384,18 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         return FQ_OK;
     }
 
-    if (M >= 2 && M <= 4 && K > 0 && packable(dtype) &&
+    // Q4_0 on the band kernel below: rows that start 16-byte aligned (K a
+    // multiple of 256), 5..16 tokens, or 4 from 16 MB (below, the kernels
+    // further down take M = 4 0.4-0.7 us faster), and at most one band of
+    // 64 rows per CU or at least eight (18944 rows leave a second, mostly
+    // idle round: 28.6 against 24.8-27.6 us at M = 4..8; 152064 rows at M =
+    // 4..16 129-135 against 151-158 us)
+    const long q40_bands = ((long)N + 16 * fq::mmqs_max_tiles() - 1) / (16 * fq::mmqs_max_tiles());
+    const bool q40_band = dtype == FQ_DTYPE_Q4_0 && K % 256 == 0 &&
+                          (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                          (M >= 5 || (int64_t)N * (K / 32) * 18 >= (16 << 20)) &&
+                          (q40_bands <= di.cus || q40_bands >= 8L * di.cus);
+    if (M >= 2 && M <= (q40_band ? 3 : 4) && K > 0 && packable(dtype) &&
         (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
         // two to four tokens: the same kernel dots each weight unit it reads
         // with every token's limbs, K split into slabs where the tokens'
@@ -396,7 +408,8 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     }
 
     if (fq::mmqs_supported((int)dtype) && M >= 4 && M <= 16 && K > 0 &&
-        N <= 16 * fq::mmqs_max_tiles() * di.cus) {
+        (dtype == FQ_DTYPE_Q4_0 ? q40_band : N <= 16 * fq::mmqs_max_tiles() * di.cus)) {
+        // (Q4_0: see q40_band)
         // 4..16 tokens: token operands, then one pass over the weights on the
         // fp16 matrix cores, one band of rows per work-group (measured at
         // 14336 x 4096: 19.2-19.7 us for every M in 4..16, against 21-30 us on

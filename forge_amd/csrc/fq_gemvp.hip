@@ -822,10 +822,13 @@ const void* gfnt(int units, bool bias, int* gp, int* nl) {
                     case 3: return gfn_t<F, 2, 3, NT>(bias, os);
                 }
                 return nullptr;
-            } else {
-                // three and four tokens: one lane unit per lane
+            } else if constexpr (NT == 3) {
+                // three tokens: one lane unit per lane (four: the other
+                // kernels, 4096 x 4096 9.7 against 10.7 us this way)
                 *nl = 1;
                 return gfnt_one<F, NT>(units, bias, gp);
+            } else {
+                return nullptr;
             }
         }
     }

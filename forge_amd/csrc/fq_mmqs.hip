@@ -63,6 +63,7 @@ struct Band;
 template <>
 struct Band<Q4_K> {
     static constexpr int SBK = 256, PANEL = 16 * 144, PIECES = PANEL / 16;
+    static constexpr bool MIN = true;  // the -dmin m terms
     __device__ static const uint8_t* piece(const uint8_t* row0, int row_bytes, int sb, int p) {
         const int rr = p / 9;
         return row0 + (size_t)rr * row_bytes + 144 * sb + 16 * (p - 9 * rr);
@@ -81,6 +82,46 @@ struct Band<Q4_K> {
         Fmt<Q4_K>::scale_min(uint4{h.x, h.y, h.z, h.w}, g, sa, ma, sb, mb);
         const float d = f16_hw(h.x & 0xFFFFu), dmin = f16_hw(h.x >> 16);
         return float4{d * (float)sa, d * (float)sb, -dmin * (float)ma, -dmin * (float)mb};
+    }
+};
+
+// Q4_0: eight 18-byte blocks (d | qs[16], element j the low nibble of qs[j],
+// j + 16 the high one) make the same 144 bytes per 256 elements and row, so
+// the panels and their loads are those of Q4_K (the host takes this kernel
+// only for rows that start 16-byte aligned: K a multiple of 256 and an
+// aligned base).  Chunk g = blocks 2 g and 2 g + 1: lane (r, q) takes
+// elements 8 q .. 8 q + 7 of each, the low (q < 2) or high nibbles of qs
+// bytes 8 (q & 1) .. + 7, as quant - 8; the coefficients are the blocks'
+// scales d, and there is no minimum term.
+template <>
+struct Band<Q4_0> {
+    static constexpr int SBK = 256, PANEL = 16 * 144, PIECES = PANEL / 16;
+    static constexpr bool MIN = false;
+    __device__ static const uint8_t* piece(const uint8_t* row0, int row_bytes, int sb, int p) {
+        return Band<Q4_K>::piece(row0, row_bytes, sb, p);
+    }
+    // eight bytes of the panel at byte offset o, o = 2 (mod 4) when ODD2
+    template <bool ODD2>
+    __device__ static fq_u32x2 ld8(const uint8_t* panel, int o) {
+        if constexpr (ODD2) {
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(panel + o - 2);
+            return fq_u32x2{__builtin_amdgcn_alignbyte(w[1], w[0], 2),
+                            __builtin_amdgcn_alignbyte(w[2], w[1], 2)};
+        } else {
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(panel + o);
+            return fq_u32x2{w[0], w[1]};
+        }
+    }
+    __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
+        // block 2 g + s of row r starts at 144 r + 36 g + 18 s; its qs at + 2
+        const int o = 144 * r + 36 * g + 2 + 8 * (q & 1), sh = q < 2 ? 0 : 4;
+        const fq_u32x2 b0 = ld8<true>(panel, o), b1 = ld8<false>(panel, o + 18);
+        a0 = nib8(b0.x, b0.y, sh, (_Float16)1032.0f);
+        a1 = nib8(b1.x, b1.y, sh, (_Float16)1032.0f);
+    }
+    __device__ static float4 coef4(const uint8_t* panel, int g, int r) {
+        const uint16_t* d = reinterpret_cast<const uint16_t*>(panel + 144 * r + 36 * g);
+        return float4{f16_hw(d[0]), f16_hw(d[9]), 0.0f, 0.0f};
     }
 };
 
@@ -224,8 +265,10 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
                 for (int i = 0; i < 4; ++i) {
                     float s = a0v[i] * d0[i];
                     s = __builtin_fmaf(a1v[i], d1[i], s);
-                    s = __builtin_fmaf(b0v[i], S0, s);
-                    s = __builtin_fmaf(b1v[i], S1, s);
+                    if constexpr (B::MIN) {
+                        s = __builtin_fmaf(b0v[i], S0, s);
+                        s = __builtin_fmaf(b1v[i], S1, s);
+                    }
                     acc[t][i] = __builtin_fmaf(s, p2, acc[t][i]);
                 }
             }
@@ -282,7 +325,7 @@ const void* sfn_tw(int tw, bool bias) {
 
 }  // namespace
 
-bool mmqs_supported(int dtype) { return dtype == Q4_K; }
+bool mmqs_supported(int dtype) { return dtype == Q4_K || dtype == Q4_0; }
 
 // Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
 // rows).
@@ -296,6 +339,14 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int
         fn = wg == 256   ? sfn_tw<Q4_K, 256>(tw, a.bias_mode != 0)
              : wg == 1024 ? sfn_tw<Q4_K, 1024>(tw, a.bias_mode != 0)
                           : sfn_tw<Q4_K, 512>(tw, a.bias_mode != 0);
+    } else if (dtype == Q4_0) {
+        // rows must start 16-byte aligned (the panel loads are 16 bytes)
+        if (a.K % 256 != 0 || a.row_bytes % 16 != 0 ||
+            (reinterpret_cast<uintptr_t>(a.w) & 15) != 0)
+            return hipErrorInvalidValue;
+        fn = wg == 256   ? sfn_tw<Q4_0, 256>(tw, a.bias_mode != 0)
+             : wg == 1024 ? sfn_tw<Q4_0, 1024>(tw, a.bias_mode != 0)
+                          : sfn_tw<Q4_0, 512>(tw, a.bias_mode != 0);
     }
     if (!fn) return hipErrorInvalidValue;
     const int nsb = a.K / 256;

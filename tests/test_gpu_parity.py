@@ -164,6 +164,39 @@ def test_small_batch_config3(M):
     check_shape(F.Q4_K, 14336, 4096, M, seed=3000 + M, what=f"cfg3 M={M}")
 
 
+@pytest.mark.parametrize("M", [4, 5, 8, 13, 16])
+@pytest.mark.parametrize("N,K", [(3584, 18944), (1000, 4096), (4099, 2048), (131072, 256)])
+def test_q4_0_small_batch_band_kernel(N, K, M):
+    # Q4_0, 4..16 tokens (M = 4 only from 16 MB; under that the other kernels):
+    # the fp16 band kernel over 144-byte groups of eight blocks (3584 x
+    # 18944: K split into slabs; 4099 rows: a ragged last tile; 131072 rows:
+    # eight bands per CU), each bias form added after the sum; at a 2-byte
+    # offset base or K = 4096 + 32 the rows are not 16-byte aligned and the
+    # call takes the other kernels
+    w = synth.make_weights(F.Q4_0, N, K, seed=N + M)
+    x = synth.make_x(M, K, N + M + 1)
+    y = run(F.Q4_0, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(F.Q4_0, w, min(N, 4096), K))))
+    assert_close(y, oracle.matmul_f64(F.Q4_0, x, w, N, K), x, np.array([deq_max]),
+                 f"Q4_0 M={M} {N}x{K}")
+    b1 = torch.linspace(-1, 1, N)
+    np.testing.assert_allclose(run(F.Q4_0, w, x, N, K, bias=b1), y + b1.numpy(), rtol=1e-6,
+                               atol=1e-6)
+    b2 = torch.randn(M, N)
+    np.testing.assert_allclose(run(F.Q4_0, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
+                               atol=1e-6)
+    if K == 4096:
+        y2 = run(F.Q4_0, w, x, N, K, offset=2)
+        assert_close(y2, oracle.matmul_f64(F.Q4_0, x, w, N, K), x, np.array([deq_max]),
+                     f"Q4_0 M={M} {N}x{K} offset 2")
+        K2 = K + 32
+        w2 = synth.make_weights(F.Q4_0, N, K2, seed=N + M + 2)
+        x2 = synth.make_x(M, K2, N + M + 3)
+        assert_close(run(F.Q4_0, w2, x2, N, K2), oracle.matmul_f64(F.Q4_0, x2, w2, N, K2), x2,
+                     np.array([float(np.max(np.abs(oracle.dequant(F.Q4_0, w2, N, K2))))]),
+                     f"Q4_0 M={M} {N}x{K2}")
+
+
 @pytest.mark.parametrize("M", [2, 3, 4])
 @pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K])
 @pytest.mark.parametrize("N,K", [(4099, 4096), (2113, 7168), (1500, 18944)])
@@ -172,8 +205,9 @@ def test_few_tokens_batch1_kernel(dtype, N, K, M):
     # M > 1 take other kernels): the batch-1 kernel
     # dots each weight unit with every token's limbs (Q4_K and Q6_K: up to
     # three tokens).  Q4_0 and Q4_1 rows of 65-192 blocks take two lane units
-    # per lane at one and two tokens, one at three and four (so those rows'
-    # K-slices, and their summation order, differ from the M = 1 call's).
+    # per lane at one and two tokens, one at three (so those rows' K-slices,
+    # and their summation order, differ from the M = 1 call's), and other
+    # kernels at four.
     # Otherwise each token's arithmetic and summation order are the batch-1
     # kernel's, so token t's row equals the M = 1 result bit for bit; the
     # oracle pins every case.  Every bias form is added after the
