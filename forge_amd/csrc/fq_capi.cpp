@@ -386,16 +386,19 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
 
     // Q4_0 on the band kernel below: rows that start 16-byte aligned (K a
     // multiple of 256), 5..16 tokens, or 4 from 16 MB (below, the kernels
-    // further down take M = 4 0.4-0.7 us faster), and at most one band of
+    // further down take M = 4 0.4-0.7 us faster), or 3 from 16 MB with K of
+    // 14336 and more (3584 x 18944: 26.4 us on the batch-1 kernel), and at
+    // most one band of
     // 64 rows per CU or at least eight (18944 rows leave a second, mostly
     // idle round: 28.6 against 24.8-27.6 us at M = 4..8; 152064 rows at M =
     // 4..16 129-135 against 151-158 us)
     const long q40_bands = ((long)N + 16 * fq::mmqs_max_tiles() - 1) / (16 * fq::mmqs_max_tiles());
     const bool q40_band = dtype == FQ_DTYPE_Q4_0 && K % 256 == 0 &&
                           (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
-                          (M >= 5 || (int64_t)N * (K / 32) * 18 >= (16 << 20)) &&
+                          (M >= 5 || ((M == 4 || (M == 3 && K >= 14336)) &&
+                                      (int64_t)N * (K / 32) * 18 >= (16 << 20))) &&
                           (q40_bands <= di.cus || q40_bands >= 8L * di.cus);
-    if (M >= 2 && M <= (q40_band ? 3 : 4) && K > 0 && packable(dtype) &&
+    if (M >= 2 && M <= 4 && !q40_band && K > 0 && packable(dtype) &&
         (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
         // two to four tokens: the same kernel dots each weight unit it reads
         // with every token's limbs, K split into slabs where the tokens'
@@ -407,7 +410,7 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
-    if (fq::mmqs_supported((int)dtype) && M >= 4 && M <= 16 && K > 0 &&
+    if (fq::mmqs_supported((int)dtype) && M >= (q40_band ? 3 : 4) && M <= 16 && K > 0 &&
         (dtype == FQ_DTYPE_Q4_0 ? q40_band : N <= 16 * fq::mmqs_max_tiles() * di.cus)) {
         // (Q4_0: see q40_band)
         // 4..16 tokens: token operands, then one pass over the weights on the

@@ -164,10 +164,11 @@ def test_small_batch_config3(M):
     check_shape(F.Q4_K, 14336, 4096, M, seed=3000 + M, what=f"cfg3 M={M}")
 
 
-@pytest.mark.parametrize("M", [4, 5, 8, 13, 16])
+@pytest.mark.parametrize("M", [3, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("N,K", [(3584, 18944), (1000, 4096), (4099, 2048), (131072, 256)])
 def test_q4_0_small_batch_band_kernel(N, K, M):
-    # Q4_0, 4..16 tokens (M = 4 only from 16 MB; under that the other kernels):
+    # Q4_0, 4..16 tokens (M = 4 only from 16 MB, M = 3 from 16 MB at K >=
+    # 14336; otherwise the other kernels):
     # the fp16 band kernel over 144-byte groups of eight blocks (3584 x
     # 18944: K split into slabs; 4099 rows: a ragged last tile; 131072 rows:
     # eight bands per CU), each bias form added after the sum; at a 2-byte
