@@ -6,7 +6,7 @@
 // matrices of 64k rows and more on the aligned layout, the row-step kernels
 // of fq_gemv1.hip under about 4 MB of weights); M = 2..4
 // the same batch-1 kernels with each weight unit dotted with every token;
-// Q4_K and Q4_0 M = 4..16 the band kernel of fq_mmqs.hip (Q6_K M = 4, 5 from
+// Q4_K, Q4_0 and Q8_0 M = 4..16 the band kernel of fq_mmqs.hip (Q6_K M = 4, 5 from
 // 24 MB: three tokens, then the rest); M > 32 the prefill kernel
 // of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --
 // the reference's batched GEMV (1 < M <= 32) and dequant + GEMM prefill
@@ -184,8 +184,8 @@ MmqPlan plan_mmq(int M, int K, int N, int cus) {
 // summed in split order).  Measured at 3584 x 18944 (M = 4 / 16): 30.3 /
 // 30.8 us unsplit on 16-row bands, 27.1 / 28.0 us on 64-row bands in four
 // splits; at K = 4096 every split measured slower.
-int mmqs_plan(int N, int K, int cus, int* rows_per_wg) {
-    const int nsb = K / 256, mt = fq::mmqs_max_tiles();
+int mmqs_plan(int N, int K, int cus, int* rows_per_wg, int mt) {
+    const int nsb = K / 256;
     const long bands4 = (N + 16 * mt - 1) / (16 * mt);
     if (nsb >= 32 && 2 * bands4 <= cus) {
         *rows_per_wg = 16 * mt;
@@ -199,10 +199,10 @@ int mmqs_plan(int N, int K, int cus, int* rows_per_wg) {
 
 // Workspace bytes of a band-kernel call: the token operands of plan_mmq's
 // single token tile and, when K is split, the slabs.
-size_t mmqs_need(int M, int K, int N, int cus) {
+size_t mmqs_need(int M, int K, int N, int cus, int mt) {
     const MmqPlan pl = plan_mmq(M, K, N, cus);
     int rpw = 0;
-    const int splits = mmqs_plan(N, K, cus, &rpw);
+    const int splits = mmqs_plan(N, K, cus, &rpw, mt);
     const size_t part_b = splits > 1 ? (size_t)splits * M * N * 4 : 0;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     return 256 + al(pl.xop_b) + al(pl.xsum_b) + al(pl.ex_b) + al(part_b);
@@ -384,21 +384,27 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         return FQ_OK;
     }
 
-    // Q4_0 on the band kernel below: rows that start 16-byte aligned (K a
-    // multiple of 256), 5..16 tokens, or 4 from 16 MB (below, the kernels
-    // further down take M = 4 0.4-0.7 us faster), or 3 from 16 MB with K of
-    // 14336 and more (3584 x 18944: 26.4 us on the batch-1 kernel), and at
-    // most one band of
-    // 64 rows per CU or at least eight (18944 rows leave a second, mostly
-    // idle round: 28.6 against 24.8-27.6 us at M = 4..8; 152064 rows at M =
-    // 4..16 129-135 against 151-158 us)
-    const long q40_bands = ((long)N + 16 * fq::mmqs_max_tiles() - 1) / (16 * fq::mmqs_max_tiles());
-    const bool q40_band = dtype == FQ_DTYPE_Q4_0 && K % 256 == 0 &&
+    // Q4_0 and Q8_0 on the band kernel below: rows that start 16-byte aligned
+    // (K a multiple of 256), 5..16 tokens, or 4 from 16 MB (below, the
+    // kernels further down take M = 4 0.4-0.7 us faster for Q4_0; Q8_0 only
+    // while the bands number at most one per CU: lm_head 157 us on the
+    // batch-1 kernel against 173), or, Q4_0 only, 3 from 16 MB with K of
+    // 14336 and more (3584 x 18944: 26.4 us on the batch-1 kernel).  Q4_0
+    // needs at most one band per CU or at least eight (18944 rows, 296 bands
+    // of 64, leave a second, mostly idle round: 28.6 against 24.8-27.6 us at
+    // M = 4..8; 152064 rows at M = 4..16 129-135 against 151-158 us); Q8_0
+    // takes any count (the fp16 MFMA path is slower at every one measured:
+    // 14336 x 4096 at M = 8 24.1 against 37.6 us)
+    const int bmt = fq::mmqs_max_tiles((int)dtype);
+    const long bands = ((long)N + 16 * bmt - 1) / (16 * bmt);
+    const bool blk_band = (dtype == FQ_DTYPE_Q4_0 || dtype == FQ_DTYPE_Q8_0) && K % 256 == 0 &&
                           (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
-                          (M >= 5 || ((M == 4 || (M == 3 && K >= 14336)) &&
-                                      (int64_t)N * (K / 32) * 18 >= (16 << 20))) &&
-                          (q40_bands <= di.cus || q40_bands >= 8L * di.cus);
-    if (M >= 2 && M <= 4 && !q40_band && K > 0 && packable(dtype) &&
+                          (M >= 5 ||
+                           ((M == 4 ? dtype == FQ_DTYPE_Q4_0 || bands <= di.cus
+                                    : M == 3 && dtype == FQ_DTYPE_Q4_0 && K >= 14336) &&
+                            (int64_t)N * (K / g.be) * g.bb >= (16 << 20))) &&
+                          (dtype == FQ_DTYPE_Q8_0 || bands <= di.cus || bands >= 8L * di.cus);
+    if (M >= 2 && M <= 4 && !blk_band && K > 0 && packable(dtype) &&
         (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
         // two to four tokens: the same kernel dots each weight unit it reads
         // with every token's limbs, K split into slabs where the tokens'
@@ -410,9 +416,9 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
-    if (fq::mmqs_supported((int)dtype) && M >= (q40_band ? 3 : 4) && M <= 16 && K > 0 &&
-        (dtype == FQ_DTYPE_Q4_0 ? q40_band : N <= 16 * fq::mmqs_max_tiles() * di.cus)) {
-        // (Q4_0: see q40_band)
+    if (fq::mmqs_supported((int)dtype) && M >= (blk_band ? 3 : 4) && M <= 16 && K > 0 &&
+        (dtype == FQ_DTYPE_Q4_K ? N <= 16 * bmt * di.cus : blk_band)) {
+        // (Q4_0, Q8_0: see blk_band)
         // 4..16 tokens: token operands, then one pass over the weights on the
         // fp16 matrix cores, one band of rows per work-group (measured at
         // 14336 x 4096: 19.2-19.7 us for every M in 4..16, against 21-30 us on
@@ -423,8 +429,8 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         const MmqPlan pl = plan_mmq(M, K, N, di.cus);
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
         int rpw = 0;
-        const int splits = mmqs_plan(N, K, di.cus, &rpw);
-        const size_t need = mmqs_need(M, K, N, di.cus);
+        const int splits = mmqs_plan(N, K, di.cus, &rpw, bmt);
+        const size_t need = mmqs_need(M, K, N, di.cus, bmt);
         std::unique_ptr<StreamScratch::Lease> lease;
         uint8_t* buf = fixed;
         if (fixed) {
@@ -1168,7 +1174,8 @@ int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
     for (int n = N_max; n > 0; n = n > 128 ? ((n - 1) / 128) * 128 : 0) {
         for (int m = 2; m <= M_max; ++m) {
             need0 = std::max(need0, plan_mmq(m, K_max, n, di.cus).total);
-            if (m >= 4 && m <= 16 && Kp > 0) need0 = std::max(need0, mmqs_need(m, Kp, n, di.cus));
+            if (m >= 3 && m <= 16 && Kp > 0)  // band kernel, four- and two-tile bands
+                for (int mt : {4, 2}) need0 = std::max(need0, mmqs_need(m, Kp, n, di.cus, mt));
             if (m > 32 && Kp > 0) need0 = std::max(need0, plan_mmqp(m, Kp, n, di.cus, true).total);
             // the batch-1 kernel's K-split slabs for 2..4 tokens (at most 8)
             if (m <= 4) need0 = std::max(need0, (size_t)8 * m * n * sizeof(float));

@@ -112,7 +112,7 @@ hipError_t launch_mmq(int dtype, const MmqArgs& a, int shape, int gx, int gy, in
 // the token operands of launch_xprep (one token tile), bands of rows_per_wg
 // rows (at most 16 mmqs_max_tiles()) per work-group
 bool mmqs_supported(int dtype);
-int mmqs_max_tiles();
+int mmqs_max_tiles(int dtype);  // 16-row tiles per band
 // splits > 1: K split over blockIdx.y into a.part slabs (super-blocks
 // ceil(K/256 / splits) each), then launch_reduce adds them and the bias
 hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int splits,

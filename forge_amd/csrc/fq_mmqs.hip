@@ -62,12 +62,9 @@ struct Band;
 // bytes.
 template <>
 struct Band<Q4_K> {
-    static constexpr int SBK = 256, PANEL = 16 * 144, PIECES = PANEL / 16;
+    // SBB bytes of a row per 256 elements; NPL 16-byte pieces per lane
+    static constexpr int SBK = 256, SBB = 144, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 3;
     static constexpr bool MIN = true;  // the -dmin m terms
-    __device__ static const uint8_t* piece(const uint8_t* row0, int row_bytes, int sb, int p) {
-        const int rr = p / 9;
-        return row0 + (size_t)rr * row_bytes + 144 * sb + 16 * (p - 9 * rr);
-    }
     __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
         const fq_u32x2 qs =
             *reinterpret_cast<const fq_u32x2*>(panel + 144 * r + 16 + 32 * g + 8 * q);
@@ -85,6 +82,20 @@ struct Band<Q4_K> {
     }
 };
 
+// Eight bytes of a panel at byte offset o, o = 2 (mod 4) when ODD2 (else a
+// multiple of 4).
+template <bool ODD2>
+__device__ __forceinline__ fq_u32x2 pan_ld8(const uint8_t* panel, int o) {
+    if constexpr (ODD2) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(panel + o - 2);
+        return fq_u32x2{__builtin_amdgcn_alignbyte(w[1], w[0], 2),
+                        __builtin_amdgcn_alignbyte(w[2], w[1], 2)};
+    } else {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(panel + o);
+        return fq_u32x2{w[0], w[1]};
+    }
+}
+
 // Q4_0: eight 18-byte blocks (d | qs[16], element j the low nibble of qs[j],
 // j + 16 the high one) make the same 144 bytes per 256 elements and row, so
 // the panels and their loads are those of Q4_K (the host takes this kernel
@@ -95,27 +106,12 @@ struct Band<Q4_K> {
 // scales d, and there is no minimum term.
 template <>
 struct Band<Q4_0> {
-    static constexpr int SBK = 256, PANEL = 16 * 144, PIECES = PANEL / 16;
+    static constexpr int SBK = 256, SBB = 144, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 3;
     static constexpr bool MIN = false;
-    __device__ static const uint8_t* piece(const uint8_t* row0, int row_bytes, int sb, int p) {
-        return Band<Q4_K>::piece(row0, row_bytes, sb, p);
-    }
-    // eight bytes of the panel at byte offset o, o = 2 (mod 4) when ODD2
-    template <bool ODD2>
-    __device__ static fq_u32x2 ld8(const uint8_t* panel, int o) {
-        if constexpr (ODD2) {
-            const uint32_t* w = reinterpret_cast<const uint32_t*>(panel + o - 2);
-            return fq_u32x2{__builtin_amdgcn_alignbyte(w[1], w[0], 2),
-                            __builtin_amdgcn_alignbyte(w[2], w[1], 2)};
-        } else {
-            const uint32_t* w = reinterpret_cast<const uint32_t*>(panel + o);
-            return fq_u32x2{w[0], w[1]};
-        }
-    }
     __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
         // block 2 g + s of row r starts at 144 r + 36 g + 18 s; its qs at + 2
         const int o = 144 * r + 36 * g + 2 + 8 * (q & 1), sh = q < 2 ? 0 : 4;
-        const fq_u32x2 b0 = ld8<true>(panel, o), b1 = ld8<false>(panel, o + 18);
+        const fq_u32x2 b0 = pan_ld8<true>(panel, o), b1 = pan_ld8<false>(panel, o + 18);
         a0 = nib8(b0.x, b0.y, sh, (_Float16)1032.0f);
         a1 = nib8(b1.x, b1.y, sh, (_Float16)1032.0f);
     }
@@ -125,7 +121,27 @@ struct Band<Q4_0> {
     }
 };
 
-constexpr int NPL = 3;  // 16-byte pieces per lane per panel (144 / 64, rounded up)
+// Q8_0: eight 34-byte blocks (d | qs[32] int8) are 272 bytes per 256
+// elements and row (16-byte aligned on the same conditions as Q4_0), a
+// 16 x 272-byte panel of 17 pieces per row.  Chunk g = blocks 2 g and 2 g + 1:
+// lane (r, q) takes their qs bytes 8 q .. 8 q + 7 as fp16 (the sign bit
+// flipped and 1152 subtracted: exact); the coefficients are the scales d.
+template <>
+struct Band<Q8_0> {
+    static constexpr int SBK = 256, SBB = 272, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 5;
+    static constexpr bool MIN = false;
+    __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
+        // block 2 g + s of row r starts at 272 r + 68 g + 34 s; its qs at + 2
+        const int o = SBB * r + 68 * g + 2 + 8 * q;
+        const fq_u32x2 b0 = pan_ld8<true>(panel, o), b1 = pan_ld8<false>(panel, o + 34);
+        a0 = byte8(b0.x ^ 0x80808080u, b0.y ^ 0x80808080u, (_Float16)1152.0f);
+        a1 = byte8(b1.x ^ 0x80808080u, b1.y ^ 0x80808080u, (_Float16)1152.0f);
+    }
+    __device__ static float4 coef4(const uint8_t* panel, int g, int r) {
+        const uint16_t* d = reinterpret_cast<const uint16_t*>(panel + SBB * r + 68 * g);
+        return float4{f16_hw(d[0]), f16_hw(d[17]), 0.0f, 0.0f};
+    }
+};
 
 template <int F, int TW, int WG, bool BIAS>
 __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, int sb_per_split) {
@@ -153,6 +169,7 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
     const uint8_t* prow[TW];
 #pragma unroll
     for (int t = 0; t < TW; ++t) prow[t] = a.w + (size_t)min(lo + 16 * t, a.N - 1) * a.row_bytes;
+    constexpr int NPL = B::NPL, PPR = B::SBB / 16;  // pieces per lane, per panel row
     int pp[NPL], rmax[TW];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) pp[i] = min(lane + 64 * i, B::PIECES - 1);
@@ -169,9 +186,9 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
         for (int t = 0; t < TW; ++t)
 #pragma unroll
             for (int i = 0; i < NPL; ++i) {
-                const int rr = min(pp[i] / 9, rmax[t]);  // rows past N repeat the last
-                const uint8_t* p = prow[t] + (size_t)rr * a.row_bytes + 144 * sb +
-                                   16 * (pp[i] - 9 * (pp[i] / 9));
+                const int rr = min(pp[i] / PPR, rmax[t]);  // rows past N repeat the last
+                const uint8_t* p = prow[t] + (size_t)rr * a.row_bytes + B::SBB * sb +
+                                   16 * (pp[i] - PPR * (pp[i] / PPR));
                 pv[t][i] = __builtin_nontemporal_load(reinterpret_cast<const fq_u32x4*>(p));
             }
     };
@@ -314,7 +331,7 @@ const void* sfn_tw(int tw, bool bias) {
         case 1: return sfn<F, 1, WG>(bias);
         case 2: return sfn<F, 2, WG>(bias);
     }
-    if constexpr (WG <= 512) {
+    if constexpr (WG <= 512 && F != Q8_0) {  // Q8_0: two tiles (LDS)
         switch (tw) {
             case 3: return sfn<F, 3, WG>(bias);
             case 4: return sfn<F, 4, WG>(bias);
@@ -325,11 +342,11 @@ const void* sfn_tw(int tw, bool bias) {
 
 }  // namespace
 
-bool mmqs_supported(int dtype) { return dtype == Q4_K || dtype == Q4_0; }
+bool mmqs_supported(int dtype) { return dtype == Q4_K || dtype == Q4_0 || dtype == Q8_0; }
 
 // Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
-// rows).
-int mmqs_max_tiles() { return 4; }
+// rows): Q8_0's 272-byte panels fit two per wave in LDS at 512 threads.
+int mmqs_max_tiles(int dtype) { return dtype == Q8_0 ? 2 : 4; }
 
 hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int splits,
                        hipStream_t st) {
@@ -339,14 +356,13 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int
         fn = wg == 256   ? sfn_tw<Q4_K, 256>(tw, a.bias_mode != 0)
              : wg == 1024 ? sfn_tw<Q4_K, 1024>(tw, a.bias_mode != 0)
                           : sfn_tw<Q4_K, 512>(tw, a.bias_mode != 0);
-    } else if (dtype == Q4_0) {
+    } else if (dtype == Q4_0 || dtype == Q8_0) {
         // rows must start 16-byte aligned (the panel loads are 16 bytes)
         if (a.K % 256 != 0 || a.row_bytes % 16 != 0 ||
-            (reinterpret_cast<uintptr_t>(a.w) & 15) != 0)
+            (reinterpret_cast<uintptr_t>(a.w) & 15) != 0 || wg != 512)
             return hipErrorInvalidValue;
-        fn = wg == 256   ? sfn_tw<Q4_0, 256>(tw, a.bias_mode != 0)
-             : wg == 1024 ? sfn_tw<Q4_0, 1024>(tw, a.bias_mode != 0)
-                          : sfn_tw<Q4_0, 512>(tw, a.bias_mode != 0);
+        fn = dtype == Q4_0 ? sfn_tw<Q4_0, 512>(tw, a.bias_mode != 0)
+                           : sfn_tw<Q8_0, 512>(tw, a.bias_mode != 0);
     }
     if (!fn) return hipErrorInvalidValue;
     const int nsb = a.K / 256;

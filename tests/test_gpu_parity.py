@@ -166,36 +166,38 @@ def test_small_batch_config3(M):
 
 @pytest.mark.parametrize("M", [3, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("N,K", [(3584, 18944), (1000, 4096), (4099, 2048), (131072, 256)])
-def test_q4_0_small_batch_band_kernel(N, K, M):
-    # Q4_0, 4..16 tokens (M = 4 only from 16 MB, M = 3 from 16 MB at K >=
-    # 14336; otherwise the other kernels):
-    # the fp16 band kernel over 144-byte groups of eight blocks (3584 x
-    # 18944: K split into slabs; 4099 rows: a ragged last tile; 131072 rows:
-    # eight bands per CU), each bias form added after the sum; at a 2-byte
-    # offset base or K = 4096 + 32 the rows are not 16-byte aligned and the
-    # call takes the other kernels
-    w = synth.make_weights(F.Q4_0, N, K, seed=N + M)
+@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q8_0])
+def test_block_formats_small_batch_band_kernel(dtype, N, K, M):
+    # Q4_0 / Q8_0, 4..16 tokens (M = 4 from 16 MB, M = 3 from 16 MB at K >=
+    # 14336; otherwise the other kernels): the fp16 band kernel over groups
+    # of eight blocks (144 / 272 bytes; 3584 x 18944: K split into slabs;
+    # 4099 rows: a ragged last tile; 131072 rows: eight bands and more per
+    # CU), each bias form added after the sum; at a 2-byte offset base or K =
+    # 4096 + 32 the rows are not 16-byte aligned and the call takes the other
+    # kernels
+    name = F.fmt(dtype).name
+    w = synth.make_weights(dtype, N, K, seed=N + M)
     x = synth.make_x(M, K, N + M + 1)
-    y = run(F.Q4_0, w, x, N, K)
-    deq_max = float(np.max(np.abs(oracle.dequant(F.Q4_0, w, min(N, 4096), K))))
-    assert_close(y, oracle.matmul_f64(F.Q4_0, x, w, N, K), x, np.array([deq_max]),
-                 f"Q4_0 M={M} {N}x{K}")
+    y = run(dtype, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(dtype, w, min(N, 4096), K))))
+    assert_close(y, oracle.matmul_f64(dtype, x, w, N, K), x, np.array([deq_max]),
+                 f"{name} M={M} {N}x{K}")
     b1 = torch.linspace(-1, 1, N)
-    np.testing.assert_allclose(run(F.Q4_0, w, x, N, K, bias=b1), y + b1.numpy(), rtol=1e-6,
+    np.testing.assert_allclose(run(dtype, w, x, N, K, bias=b1), y + b1.numpy(), rtol=1e-6,
                                atol=1e-6)
     b2 = torch.randn(M, N)
-    np.testing.assert_allclose(run(F.Q4_0, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
+    np.testing.assert_allclose(run(dtype, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
                                atol=1e-6)
     if K == 4096:
-        y2 = run(F.Q4_0, w, x, N, K, offset=2)
-        assert_close(y2, oracle.matmul_f64(F.Q4_0, x, w, N, K), x, np.array([deq_max]),
-                     f"Q4_0 M={M} {N}x{K} offset 2")
+        y2 = run(dtype, w, x, N, K, offset=2)
+        assert_close(y2, oracle.matmul_f64(dtype, x, w, N, K), x, np.array([deq_max]),
+                     f"{name} M={M} {N}x{K} offset 2")
         K2 = K + 32
-        w2 = synth.make_weights(F.Q4_0, N, K2, seed=N + M + 2)
+        w2 = synth.make_weights(dtype, N, K2, seed=N + M + 2)
         x2 = synth.make_x(M, K2, N + M + 3)
-        assert_close(run(F.Q4_0, w2, x2, N, K2), oracle.matmul_f64(F.Q4_0, x2, w2, N, K2), x2,
-                     np.array([float(np.max(np.abs(oracle.dequant(F.Q4_0, w2, N, K2))))]),
-                     f"Q4_0 M={M} {N}x{K2}")
+        assert_close(run(dtype, w2, x2, N, K2), oracle.matmul_f64(dtype, x2, w2, N, K2), x2,
+                     np.array([float(np.max(np.abs(oracle.dequant(dtype, w2, N, K2))))]),
+                     f"{name} M={M} {N}x{K2}")
 
 
 @pytest.mark.parametrize("M", [2, 3, 4])
@@ -224,7 +226,10 @@ def test_few_tokens_batch1_kernel(dtype, N, K, M):
     fm = F.fmt(dtype)
     units = K // 32  # 32-element units
     big = dtype == F.Q6_K or N * (K // fm.block_elems) * fm.block_bytes >= 8 << 20
-    batch1 = (big and K != 18944 and not (M == 4 and dtype in (F.Q4_K, F.Q6_K))
+    # (Q4_0 / Q8_0 from 16 MB at M = 4: the band kernel)
+    band = (dtype in (F.Q4_0, F.Q8_0) and M == 4 and K % 256 == 0
+            and N * (K // fm.block_elems) * fm.block_bytes >= 16 << 20)
+    batch1 = (big and not band and K != 18944 and not (M == 4 and dtype in (F.Q4_K, F.Q6_K))
               and not (M > 2 and dtype in (F.Q4_0, F.Q4_1) and units > 64))
     if batch1:
         for t in range(M):
