@@ -6,7 +6,7 @@
 // matrices of 64k rows and more on the aligned layout, the row-step kernels
 // of fq_gemv1.hip under about 4 MB of weights); M = 2..4
 // the same batch-1 kernels with each weight unit dotted with every token;
-// Q4_K, Q4_0 and Q8_0 M = 4..16 the band kernel of fq_mmqs.hip (Q6_K M = 4, 5 from
+// Q4_K, Q4_0, Q4_1 and Q8_0 M = 4..16 the band kernel of fq_mmqs.hip (Q6_K M = 4, 5 from
 // 24 MB: three tokens, then the rest); M > 32 the prefill kernel
 // of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --
 // the reference's batched GEMV (1 < M <= 32) and dequant + GEMM prefill
@@ -397,11 +397,12 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     // 14336 x 4096 at M = 8 24.1 against 37.6 us)
     const int bmt = fq::mmqs_max_tiles((int)dtype);
     const long bands = ((long)N + 16 * bmt - 1) / (16 * bmt);
-    const bool blk_band = (dtype == FQ_DTYPE_Q4_0 || dtype == FQ_DTYPE_Q8_0) && K % 256 == 0 &&
+    // (Q4_1 as Q4_0)
+    const bool q4x = dtype == FQ_DTYPE_Q4_0 || dtype == FQ_DTYPE_Q4_1;
+    const bool blk_band = (q4x || dtype == FQ_DTYPE_Q8_0) && K % 256 == 0 &&
                           (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
                           (M >= 5 ||
-                           ((M == 4 ? dtype == FQ_DTYPE_Q4_0 || bands <= di.cus
-                                    : M == 3 && dtype == FQ_DTYPE_Q4_0 && K >= 14336) &&
+                           ((M == 4 ? q4x || bands <= di.cus : M == 3 && q4x && K >= 14336) &&
                             (int64_t)N * (K / g.be) * g.bb >= (16 << 20))) &&
                           (dtype == FQ_DTYPE_Q8_0 || bands <= di.cus || bands >= 8L * di.cus);
     if (M >= 2 && M <= 4 && !blk_band && K > 0 && packable(dtype) &&

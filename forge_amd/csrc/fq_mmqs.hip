@@ -121,6 +121,29 @@ struct Band<Q4_0> {
     }
 };
 
+// Q4_1: eight 20-byte blocks (d | m | qs[16], nibbles as Q4_0's, w = d q +
+// m) are 160 bytes per 256 elements and row, ten pieces per panel row.  The
+// operands are the nibbles as they stand (0 .. 15), the coefficients the
+// blocks' d and, for the sub-block sums of x, m.
+template <>
+struct Band<Q4_1> {
+    static constexpr int SBK = 256, SBB = 160, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 3;
+    static constexpr bool MIN = true;
+    __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
+        // block 2 g + s of row r starts at 160 r + 40 g + 20 s; its qs at + 4
+        const int o = SBB * r + 40 * g + 4 + 8 * (q & 1), sh = q < 2 ? 0 : 4;
+        const fq_u32x2 b0 = pan_ld8<false>(panel, o), b1 = pan_ld8<false>(panel, o + 20);
+        a0 = nib8(b0.x, b0.y, sh, (_Float16)1024.0f);
+        a1 = nib8(b1.x, b1.y, sh, (_Float16)1024.0f);
+    }
+    __device__ static float4 coef4(const uint8_t* panel, int g, int r) {
+        const uint32_t* h = reinterpret_cast<const uint32_t*>(panel + SBB * r + 40 * g);
+        const uint32_t h0 = h[0], h1 = h[5];  // d | m of the two blocks
+        return float4{f16_hw(h0 & 0xFFFFu), f16_hw(h1 & 0xFFFFu), f16_hw(h0 >> 16),
+                      f16_hw(h1 >> 16)};
+    }
+};
+
 // Q8_0: eight 34-byte blocks (d | qs[32] int8) are 272 bytes per 256
 // elements and row (16-byte aligned on the same conditions as Q4_0), a
 // 16 x 272-byte panel of 17 pieces per row.  Chunk g = blocks 2 g and 2 g + 1:
@@ -342,7 +365,9 @@ const void* sfn_tw(int tw, bool bias) {
 
 }  // namespace
 
-bool mmqs_supported(int dtype) { return dtype == Q4_K || dtype == Q4_0 || dtype == Q8_0; }
+bool mmqs_supported(int dtype) {
+    return dtype == Q4_K || dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0;
+}
 
 // Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
 // rows): Q8_0's 272-byte panels fit two per wave in LDS at 512 threads.
@@ -356,13 +381,14 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int
         fn = wg == 256   ? sfn_tw<Q4_K, 256>(tw, a.bias_mode != 0)
              : wg == 1024 ? sfn_tw<Q4_K, 1024>(tw, a.bias_mode != 0)
                           : sfn_tw<Q4_K, 512>(tw, a.bias_mode != 0);
-    } else if (dtype == Q4_0 || dtype == Q8_0) {
+    } else if (dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0) {
         // rows must start 16-byte aligned (the panel loads are 16 bytes)
         if (a.K % 256 != 0 || a.row_bytes % 16 != 0 ||
             (reinterpret_cast<uintptr_t>(a.w) & 15) != 0 || wg != 512)
             return hipErrorInvalidValue;
-        fn = dtype == Q4_0 ? sfn_tw<Q4_0, 512>(tw, a.bias_mode != 0)
-                           : sfn_tw<Q8_0, 512>(tw, a.bias_mode != 0);
+        fn = dtype == Q4_0   ? sfn_tw<Q4_0, 512>(tw, a.bias_mode != 0)
+             : dtype == Q4_1 ? sfn_tw<Q4_1, 512>(tw, a.bias_mode != 0)
+                             : sfn_tw<Q8_0, 512>(tw, a.bias_mode != 0);
     }
     if (!fn) return hipErrorInvalidValue;
     const int nsb = a.K / 256;

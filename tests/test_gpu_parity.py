@@ -166,11 +166,11 @@ def test_small_batch_config3(M):
 
 @pytest.mark.parametrize("M", [3, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("N,K", [(3584, 18944), (1000, 4096), (4099, 2048), (131072, 256)])
-@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q8_0])
+@pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0])
 def test_block_formats_small_batch_band_kernel(dtype, N, K, M):
-    # Q4_0 / Q8_0, 4..16 tokens (M = 4 from 16 MB, M = 3 from 16 MB at K >=
-    # 14336; otherwise the other kernels): the fp16 band kernel over groups
-    # of eight blocks (144 / 272 bytes; 3584 x 18944: K split into slabs;
+    # Q4_0 / Q4_1 / Q8_0, 4..16 tokens (M = 4 from 16 MB, M = 3 from 16 MB at
+    # K >= 14336 for Q4_0 and Q4_1; otherwise the other kernels): the fp16
+    # band kernel over groups of eight blocks (144 / 160 / 272 bytes; 3584 x 18944: K split into slabs;
     # 4099 rows: a ragged last tile; 131072 rows: eight bands and more per
     # CU), each bias form added after the sum; at a 2-byte offset base or K =
     # 4096 + 32 the rows are not 16-byte aligned and the call takes the other
@@ -227,7 +227,7 @@ def test_few_tokens_batch1_kernel(dtype, N, K, M):
     units = K // 32  # 32-element units
     big = dtype == F.Q6_K or N * (K // fm.block_elems) * fm.block_bytes >= 8 << 20
     # (Q4_0 / Q8_0 from 16 MB at M = 4: the band kernel)
-    band = (dtype in (F.Q4_0, F.Q8_0) and M == 4 and K % 256 == 0
+    band = (dtype in (F.Q4_0, F.Q4_1, F.Q8_0) and M == 4 and K % 256 == 0
             and N * (K // fm.block_elems) * fm.block_bytes >= 16 << 20)
     batch1 = (big and not band and K != 18944 and not (M == 4 and dtype in (F.Q4_K, F.Q6_K))
               and not (M > 2 and dtype in (F.Q4_0, F.Q4_1) and units > 64))
