@@ -6,8 +6,9 @@
 // matrices of 64k rows and more on the aligned layout, the row-step kernels
 // of fq_gemv1.hip under about 4 MB of weights); M = 2..4
 // the same batch-1 kernels with each weight unit dotted with every token;
-// Q4_K, Q4_0, Q4_1 and Q8_0 M = 4..16 the band kernel of fq_mmqs.hip (Q6_K M = 4, 5 from
-// 24 MB: three tokens, then the rest); M > 32 the prefill kernel
+// Q4_K, Q4_0, Q4_1, Q8_0 and Q6_K M = 4..16 the band kernel of fq_mmqs.hip
+// (Q6_K M = 4 on wide matrices: three tokens, then the fourth); M > 32 the
+// prefill kernel
 // of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --
 // the reference's batched GEMV (1 < M <= 32) and dequant + GEMM prefill
 // (M > 32), matmul.cpp:1150-1286 -- the int8 and fp16 MFMA kernels of
@@ -365,14 +366,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
-    if (dtype == FQ_DTYPE_Q6_K && (M == 4 || M == 5) && K > 0 &&
+    if (dtype == FQ_DTYPE_Q6_K && M == 4 && K > 0 && N > 16384 &&
         (int64_t)N * (K / g.be) * g.bb >= (24 << 20)) {
-        // four or five Q6_K tokens on 24 MB and more: three on the batch-1
-        // kernel, then the rest (its four-token form spills, and the MFMA
-        // path takes twice the three-token time: M = 4 / 5 at 3584 x 18944
-        // 59.0 / 59.1 -> 45.6 / 53.6 us, 14336 x 4096 33.8 / 41.2 -> 29.9 /
-        // 32.9, 152064 x 3584 257 -> 196 / 212; at 4096 x 4096 (14 MB) the
-        // MFMA path is faster, 13.4 against 16.7 us at M = 4)
+        // four Q6_K tokens on 24 MB and more of more than 16384 rows: three on
+        // the batch-1 kernel, then the fourth (its four-token form spills;
+        // 152064 x 3584 196-203 us against 209 on the band kernel, 18944 x
+        // 3584 34.7 against 37.3); fewer rows, and five tokens, take the band
+        // kernel below (3584 x 18944 35.0 against 45.9 this way, 14336 x 4096
+        // 27.8 against 30.8, lm_head at M = 5 about 211 against 222)
         for (int t0 = 0; t0 < M; t0 += 3) {
             const int m = std::min(3, M - t0);
             const int rc = run_matmul(dtype, x + (size_t)t0 * K, w,
@@ -418,7 +419,9 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     }
 
     if (fq::mmqs_supported((int)dtype) && M >= (blk_band ? 3 : 4) && M <= 16 && K > 0 &&
-        (dtype == FQ_DTYPE_Q4_K ? N <= 16 * bmt * di.cus : blk_band)) {
+        (dtype == FQ_DTYPE_Q4_K   ? N <= 16 * bmt * di.cus
+         : dtype == FQ_DTYPE_Q6_K ? (reinterpret_cast<uintptr_t>(w) & 1) == 0
+                                  : blk_band)) {
         // (Q4_0, Q8_0: see blk_band)
         // 4..16 tokens: token operands, then one pass over the weights on the
         // fp16 matrix cores, one band of rows per work-group (measured at

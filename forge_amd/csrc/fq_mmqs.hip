@@ -1,5 +1,6 @@
 // fq_mmqs.hip -- small-batch (M <= 16 tokens) matmul on the fp16 matrix
-// cores, streaming the GGUF rows once.
+// cores, streaming the GGUF rows once: Q4_K (below), and Q4_0, Q4_1, Q8_0
+// and Q6_K through their Band<> decoders further down.
 //
 // A work-group owns a band of rows, cut into TW tiles of 16; its waves split
 // the K dimension by super-blocks (super-block s goes to wave s % W), so each
@@ -52,6 +53,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <int F>
 struct Band;
 
+// SB16: 16-element sub-blocks (four 16x16x16 MFMA sub-blocks per chunk);
+// SHIFT: rows not 16-byte aligned (each row's super-block is loaded from its
+// aligned-down start, and read back at its byte shift)
+struct BandFlags {
+    static constexpr bool SB16 = false, SHIFT = false;
+};
+
 // Q4_K: one super-block of 16 rows is a 16 x 144-byte panel.  It is loaded
 // with 16-byte pieces (piece p of the panel: row p / 9, bytes 16 (p % 9) of
 // the row's super-block: each row a contiguous 144-byte run) and written to
@@ -61,7 +69,7 @@ struct Band;
 // 2 g, high nibbles: 2 g + 1); the row's header is the panel's first 16
 // bytes.
 template <>
-struct Band<Q4_K> {
+struct Band<Q4_K> : BandFlags {
     // SBB bytes of a row per 256 elements; NPL 16-byte pieces per lane
     static constexpr int SBK = 256, SBB = 144, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 3;
     static constexpr bool MIN = true;  // the -dmin m terms
@@ -105,7 +113,7 @@ __device__ __forceinline__ fq_u32x2 pan_ld8(const uint8_t* panel, int o) {
 // bytes 8 (q & 1) .. + 7, as quant - 8; the coefficients are the blocks'
 // scales d, and there is no minimum term.
 template <>
-struct Band<Q4_0> {
+struct Band<Q4_0> : BandFlags {
     static constexpr int SBK = 256, SBB = 144, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 3;
     static constexpr bool MIN = false;
     __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
@@ -126,7 +134,7 @@ struct Band<Q4_0> {
 // operands are the nibbles as they stand (0 .. 15), the coefficients the
 // blocks' d and, for the sub-block sums of x, m.
 template <>
-struct Band<Q4_1> {
+struct Band<Q4_1> : BandFlags {
     static constexpr int SBK = 256, SBB = 160, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 3;
     static constexpr bool MIN = true;
     __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
@@ -150,7 +158,7 @@ struct Band<Q4_1> {
 // lane (r, q) takes their qs bytes 8 q .. 8 q + 7 as fp16 (the sign bit
 // flipped and 1152 subtracted: exact); the coefficients are the scales d.
 template <>
-struct Band<Q8_0> {
+struct Band<Q8_0> : BandFlags {
     static constexpr int SBK = 256, SBB = 272, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 5;
     static constexpr bool MIN = false;
     __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
@@ -163,6 +171,53 @@ struct Band<Q8_0> {
     __device__ static float4 coef4(const uint8_t* panel, int g, int r) {
         const uint16_t* d = reinterpret_cast<const uint16_t*>(panel + SBB * r + 68 * g);
         return float4{f16_hw(d[0]), f16_hw(d[17]), 0.0f, 0.0f};
+    }
+};
+
+// A dword of the panel at byte offset o, o even.
+__device__ __forceinline__ uint32_t pan_ld4(const uint8_t* panel, int o) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(panel + (o & ~3));
+    return __builtin_amdgcn_alignbyte(w[1], w[0], o & 3);
+}
+
+// Q6_K: 210-byte super-blocks (ql[128] | qh[64] | scales[16] int8 | d),
+// rows only 2-byte aligned.  A row's super-block is loaded as the 14 aligned
+// 16-byte pieces from its aligned-down start (224 bytes: the start's shift
+// is even and at most 14), so a panel row holds it at that shift; the last
+// piece ends inside the aligned block of the row's last byte.  Element e of
+// the super-block, n = e / 128, l = e % 32, quarter u = (e % 128) / 32: the
+// low (u < 2) or high nibble of ql[64 n + 32 (u & 1) + l] and bits 2 u .. 2 u
+// + 1 of qh[32 n + l], weight d sc[e / 16] (q - 32).  Chunk g (64 elements)
+// = n = g / 2, quarters 2 (g & 1) and 2 (g & 1) + 1: sub-block s (16
+// elements) takes quarter 2 (g & 1) + s / 2, l = 16 (s & 1) + 4 q + 0 .. 3
+// for lane (r, q), as q - 32 in fp16 (1024 + q - 1056: exact).
+template <>
+struct Band<Q6_K> {
+    static constexpr bool SB16 = true, SHIFT = true, MIN = false;
+    static constexpr int SBK = 256, SBB = 210, PANEL = 16 * 224, PIECES = PANEL / 16, NPL = 4;
+    // ro: the row's byte offset in the panel (224 r + its shift)
+    __device__ static void operands(const uint8_t* panel, int ro, int g, int q, h4 (&a)[4]) {
+        const int n = g >> 1, hn = g & 1;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint32_t qh = pan_ld4(panel, ro + 128 + 32 * n + 16 * hf + 4 * q);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t ql = pan_ld4(panel, ro + 64 * n + 32 * j + 16 * hf + 4 * q);
+                const uint32_t v = ((ql >> (4 * hn)) & 0x0F0F0F0Fu) |
+                                   (((qh >> (2 * (2 * hn + j))) & 0x03030303u) << 4);
+                h2 p0, p1;
+                byte_pairs(v, (_Float16)1056.0f, p0, p1);
+                a[2 * j + hf] = h4{p0[0], p0[1], p1[0], p1[1]};
+            }
+        }
+    }
+    // d sc of the chunk's four sub-blocks
+    __device__ static float4 coef4(const uint8_t* panel, int ro, int g) {
+        const uint32_t sc = pan_ld4(panel, ro + 192 + 4 * g);
+        const float d = f16_hw(pan_ld4(panel, ro + 208) & 0xFFFFu);
+        return float4{d * (float)(int8_t)(sc & 0xFF), d * (float)(int8_t)((sc >> 8) & 0xFF),
+                      d * (float)(int8_t)((sc >> 16) & 0xFF), d * (float)(int8_t)(sc >> 24)};
     }
 };
 
@@ -192,7 +247,8 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
     const uint8_t* prow[TW];
 #pragma unroll
     for (int t = 0; t < TW; ++t) prow[t] = a.w + (size_t)min(lo + 16 * t, a.N - 1) * a.row_bytes;
-    constexpr int NPL = B::NPL, PPR = B::SBB / 16;  // pieces per lane, per panel row
+    // pieces per lane, per panel row
+    constexpr int NPL = B::NPL, PPR = B::PANEL / 256;
     int pp[NPL], rmax[TW];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) pp[i] = min(lane + 64 * i, B::PIECES - 1);
@@ -210,15 +266,29 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
 #pragma unroll
             for (int i = 0; i < NPL; ++i) {
                 const int rr = min(pp[i] / PPR, rmax[t]);  // rows past N repeat the last
-                const uint8_t* p = prow[t] + (size_t)rr * a.row_bytes + B::SBB * sb +
-                                   16 * (pp[i] - PPR * (pp[i] / PPR));
+                const uint8_t* rs = prow[t] + (size_t)rr * a.row_bytes + B::SBB * sb;
+                if constexpr (B::SHIFT) rs -= reinterpret_cast<uintptr_t>(rs) & 15;
+                const uint8_t* p = rs + 16 * (pp[i] - PPR * (pp[i] / PPR));
                 pv[t][i] = __builtin_nontemporal_load(reinterpret_cast<const fq_u32x4*>(p));
             }
     };
 
+    // SB = 32: x_hi, x_lo of sub-block 0, then of 1, eight halves per lane;
+    // SB = 16: four sub-blocks' x_hi, x_lo, four halves per lane (as the
+    // halves of one 16-byte load: lane 16 g + c of each 256-half block)
     auto load_x = [&](int ch, fq_u32x4 (&xv)[4]) {
+        if constexpr (B::SB16) {
+            const fq_u32x2* x2 = reinterpret_cast<const fq_u32x2*>(a.xop);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xv[i] = xop[(size_t)ch * (XOP / 8) + 64 * i + lane];
+            for (int i = 0; i < 4; ++i) {
+                const fq_u32x2 h = x2[(size_t)ch * (XOP / 4) + 128 * i + lane];
+                const fq_u32x2 l = x2[(size_t)ch * (XOP / 4) + 128 * i + 64 + lane];
+                xv[i] = fq_u32x4{h.x, h.y, l.x, l.y};
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[i] = xop[(size_t)ch * (XOP / 8) + 64 * i + lane];
+        }
     };
 
     // exponent and the two sub-block sums of token c in chunk ch
@@ -258,9 +328,23 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
         // panels repeat the matrix's last row and their sums are never
         // written, and a branch per tile would keep the tiles' LDS reads,
         // MFMAs and FMAs from overlapping)
+        // SHIFT: the byte offset of lane row r's super-block in its panel
+        int ro[TW];
 #pragma unroll
         for (int t = 0; t < TW; ++t) {
-            const float4 cv = B::coef4(panels[wave][t], q, r);
+            ro[t] = 0;
+            if constexpr (B::SHIFT)
+                ro[t] = (int)(reinterpret_cast<uintptr_t>(prow[t] + (size_t)min(r, rmax[t]) *
+                                                                        a.row_bytes +
+                                                          B::SBB * sb) &
+                              15) +
+                        (B::PANEL / 16) * r;
+        }
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            float4 cv;
+            if constexpr (B::SB16) cv = B::coef4(panels[wave][t], ro[t], q);
+            else cv = B::coef4(panels[wave][t], q, r);
             coef[wave][t][q][0][r] = cv.x;
             coef[wave][t][q][1][r] = cv.y;
             coef[wave][t][q][2][r] = cv.z;
@@ -282,6 +366,46 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
             if (g == 2) load_panels(min(nx, nsb - 1), pv);
             const float S0 = xs.S0, S1 = xs.S1;
             const float p2 = __builtin_amdgcn_ldexpf(1.0f, xs.e);
+            if constexpr (B::SB16) {
+                // sub-block u: x_hi in the first two dwords of xv[u], x_lo in
+                // the last two
+                h4 xh[4], xl[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    xh[u] = __builtin_bit_cast(h4, fq_u32x2{xv[u].x, xv[u].y});
+                    xl[u] = __builtin_bit_cast(h4, fq_u32x2{xv[u].z, xv[u].w});
+                }
+#pragma unroll
+                for (int t = 0; t < TW; ++t) {
+                    h4 av[4];
+                    B::operands(panels[wave][t], ro[t], g, q, av);
+                    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    f32x4 d[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        d[u] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[u], xh[u], z, 0, 0, 0);
+                        d[u] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[u], xl[u], d[u], 0, 0, 0);
+                    }
+                    float cf[4][4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float4 C =
+                            *reinterpret_cast<const float4*>(&coef[wave][t][g][u][4 * q]);
+                        cf[u][0] = C.x;
+                        cf[u][1] = C.y;
+                        cf[u][2] = C.z;
+                        cf[u][3] = C.w;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float sm = cf[0][i] * d[0][i];
+                        sm = __builtin_fmaf(cf[1][i], d[1][i], sm);
+                        sm = __builtin_fmaf(cf[2][i], d[2][i], sm);
+                        sm = __builtin_fmaf(cf[3][i], d[3][i], sm);
+                        acc[t][i] = __builtin_fmaf(sm, p2, acc[t][i]);
+                    }
+                }
+            } else {
             const h8 xh0 = __builtin_bit_cast(h8, xv[0]), xl0 = __builtin_bit_cast(h8, xv[1]);
             const h8 xh1 = __builtin_bit_cast(h8, xv[2]), xl1 = __builtin_bit_cast(h8, xv[3]);
 #pragma unroll
@@ -311,6 +435,7 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
                     }
                     acc[t][i] = __builtin_fmaf(s, p2, acc[t][i]);
                 }
+            }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) xv[i] = xn[i];
@@ -354,7 +479,7 @@ const void* sfn_tw(int tw, bool bias) {
         case 1: return sfn<F, 1, WG>(bias);
         case 2: return sfn<F, 2, WG>(bias);
     }
-    if constexpr (WG <= 512 && F != Q8_0) {  // Q8_0: two tiles (LDS)
+    if constexpr (WG <= 512 && F != Q8_0 && F != Q6_K) {  // Q8_0, Q6_K: two tiles (LDS)
         switch (tw) {
             case 3: return sfn<F, 3, WG>(bias);
             case 4: return sfn<F, 4, WG>(bias);
@@ -366,12 +491,12 @@ const void* sfn_tw(int tw, bool bias) {
 }  // namespace
 
 bool mmqs_supported(int dtype) {
-    return dtype == Q4_K || dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0;
+    return dtype == Q4_K || dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0 || dtype == Q6_K;
 }
 
 // Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
 // rows): Q8_0's 272-byte panels fit two per wave in LDS at 512 threads.
-int mmqs_max_tiles(int dtype) { return dtype == Q8_0 ? 2 : 4; }
+int mmqs_max_tiles(int dtype) { return dtype == Q8_0 || dtype == Q6_K ? 2 : 4; }
 
 hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int splits,
                        hipStream_t st) {
@@ -389,6 +514,10 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int
         fn = dtype == Q4_0   ? sfn_tw<Q4_0, 512>(tw, a.bias_mode != 0)
              : dtype == Q4_1 ? sfn_tw<Q4_1, 512>(tw, a.bias_mode != 0)
                              : sfn_tw<Q8_0, 512>(tw, a.bias_mode != 0);
+    } else if (dtype == Q6_K) {  // rows at even addresses (shifts of at most 14)
+        if (a.K % 256 != 0 || (reinterpret_cast<uintptr_t>(a.w) & 1) != 0 || wg != 512)
+            return hipErrorInvalidValue;
+        fn = sfn_tw<Q6_K, 512>(tw, a.bias_mode != 0);
     }
     if (!fn) return hipErrorInvalidValue;
     const int nsb = a.K / 256;

@@ -200,6 +200,32 @@ def test_block_formats_small_batch_band_kernel(dtype, N, K, M):
                      f"{name} M={M} {N}x{K2}")
 
 
+@pytest.mark.parametrize("M", [4, 5, 9, 16])
+@pytest.mark.parametrize("N,K", [(3584, 18944), (1000, 4096), (4099, 2048), (700, 256),
+                                 (17000, 2048)])
+def test_q6k_small_batch_band_kernel(N, K, M):
+    # Q6_K, 5..16 tokens (and 4 on at most 16384 rows or under 24 MB):
+    # the fp16 band kernel over
+    # 210-byte super-blocks loaded from each row's aligned-down start and
+    # read at the row's byte shift, four 16-element sub-blocks per chunk
+    # (3584 x 18944: K split into slabs; 4099 rows: a ragged last tile), each
+    # bias form after the sum; at a 2-byte offset base every row's shift
+    # changes and the results stay bit-identical
+    w = synth.make_weights(F.Q6_K, N, K, seed=N + M + 7)
+    x = synth.make_x(M, K, N + M + 8)
+    y = run(F.Q6_K, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(F.Q6_K, w, min(N, 4096), K))))
+    assert_close(y, oracle.matmul_f64(F.Q6_K, x, w, N, K), x, np.array([deq_max]),
+                 f"Q6_K M={M} {N}x{K}")
+    np.testing.assert_array_equal(run(F.Q6_K, w, x, N, K, offset=2), y)
+    b1 = torch.linspace(-1, 1, N)
+    np.testing.assert_allclose(run(F.Q6_K, w, x, N, K, bias=b1), y + b1.numpy(), rtol=1e-6,
+                               atol=1e-6)
+    b2 = torch.randn(M, N)
+    np.testing.assert_allclose(run(F.Q6_K, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
+                               atol=1e-6)
+
+
 @pytest.mark.parametrize("M", [2, 3, 4])
 @pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K])
 @pytest.mark.parametrize("N,K", [(4099, 4096), (2113, 7168), (1500, 18944)])
@@ -319,12 +345,12 @@ def test_unaligned_weight_base(dtype):
     assert np.array_equal(y0, y2)
 
 
-@pytest.mark.parametrize("M", [4, 5])
+@pytest.mark.parametrize("M", [4])
 def test_q6k_four_five_tokens_in_groups(M):
-    # four or five Q6_K tokens on 24 MB and more run as three tokens on the
-    # batch-1 kernel, then the rest: the rows equal those separate calls bit
-    # for bit, with each bias form
-    N, K = 2000, 18944
+    # four Q6_K tokens on 24 MB and more of more than 16384 rows run as three
+    # tokens on the batch-1 kernel, then the fourth: the rows equal those
+    # separate calls bit for bit, with each bias form
+    N, K = 17000, 2048
     w = synth.make_weights(F.Q6_K, N, K, seed=M + 80)
     x = synth.make_x(M, K, M + 81)
     y = run(F.Q6_K, w, x, N, K)
