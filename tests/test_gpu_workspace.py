@@ -73,13 +73,16 @@ def test_growth_under_capture_is_refused():
 @pytest.mark.parametrize("dtype,M,K,N", [(F.Q8_0, 40, 4096, 256), (F.Q4_0, 512, 1280, 4096),
                                          (F.Q4_K, 16, 4096, 2000), (F.Q8_0, 8, 2048, 3000),
                                          (F.Q6_K, 96, 2048, 1500), (F.Q4_K, 8, 18944, 3584),
-                                         (F.Q6_K, 2, 18944, 3584), (F.Q4_0, 3, 18944, 3584)])
+                                         (F.Q6_K, 2, 18944, 3584), (F.Q4_0, 3, 18944, 3584),
+                                         (F.Q6_K, 8, 18944, 3584), (F.Q8_0, 6, 18944, 3584),
+                                         (F.Q4_1, 16, 4096, 1000)])
 def test_reserve_then_capture_first(dtype, M, K, N):
     # fq_reserve_workspace alone (no eager call first) must cover the call's
     # kernel choice: the prefill kernel (Q8_0 / Q4_0, up to 16 K-splits; Q6_K
     # with its rewritten rows), the MMQ and small-batch paths (the band
-    # kernel with K split over four slabs at 3584 x 18944) and the batch-1
-    # kernel over two or three tokens with K split into slabs.  Three
+    # kernel with K split over four slabs at 3584 x 18944, on Q4_K, Q4_0,
+    # Q4_1, Q8_0 and Q6_K) and the batch-1 kernel over two or three tokens
+    # with K split into slabs.  Three
     # replays, each checked against the eager call, with eager work between
     # them
     L = _lib.lib()
