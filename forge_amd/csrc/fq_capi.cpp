@@ -419,10 +419,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     }
 
     if (fq::mmqs_supported((int)dtype) && M >= (blk_band ? 3 : 4) && M <= 16 && K > 0 &&
-        (dtype == FQ_DTYPE_Q4_K   ? N <= 16 * bmt * di.cus
+        (dtype == FQ_DTYPE_Q4_K   ? N <= 16 * bmt * di.cus || M > 8
          : dtype == FQ_DTYPE_Q6_K ? (reinterpret_cast<uintptr_t>(w) & 1) == 0
                                   : blk_band)) {
-        // (Q4_0, Q8_0: see blk_band)
+        // (Q4_0, Q8_0: see blk_band.  Q4_K beyond one band per CU only above
+        // 8 tokens, which the int8 kernel does not take: 18944 x 3584 at M =
+        // 16 31.2 against 34.4 us on the fp16 MFMA path, 152064 x 3584 143.5
+        // against 170.4; at M = 4..8 the int8 kernel is faster, 21.1-27.5
+        // against 30.2-30.4 and 108-130 against 137-139)
         // 4..16 tokens: token operands, then one pass over the weights on the
         // fp16 matrix cores, one band of rows per work-group (measured at
         // 14336 x 4096: 19.2-19.7 us for every M in 4..16, against 21-30 us on

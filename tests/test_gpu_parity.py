@@ -226,6 +226,22 @@ def test_q6k_small_batch_band_kernel(N, K, M):
                                atol=1e-6)
 
 
+@pytest.mark.parametrize("M", [8, 9, 16])
+def test_q4k_wide_small_batch(M):
+    # Q4_K on more rows than one four-tile band per CU: the int8 kernel up to
+    # 8 tokens, the band kernel above (K = 4352: 17 super-blocks)
+    N, K = 17001, 4352
+    w = synth.make_weights(F.Q4_K, N, K, seed=M + 90)
+    x = synth.make_x(M, K, M + 91)
+    y = run(F.Q4_K, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(F.Q4_K, w, 4096, K))))
+    assert_close(y, oracle.matmul_f64(F.Q4_K, x, w, N, K), x, np.array([deq_max]),
+                 f"Q4_K M={M} {N}x{K}")
+    b2 = torch.randn(M, N)
+    np.testing.assert_allclose(run(F.Q4_K, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
+                               atol=1e-6)
+
+
 @pytest.mark.parametrize("M", [2, 3, 4])
 @pytest.mark.parametrize("dtype", [F.Q4_0, F.Q4_1, F.Q8_0, F.Q4_K, F.Q6_K])
 @pytest.mark.parametrize("N,K", [(4099, 4096), (2113, 7168), (1500, 18944)])
