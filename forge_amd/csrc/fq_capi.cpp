@@ -6,7 +6,7 @@
 // matrices of 64k rows and more on the aligned layout, the row-step kernels
 // of fq_gemv1.hip under about 4 MB of weights); M = 2..4
 // the same batch-1 kernels with each weight unit dotted with every token;
-// Q4_K, Q4_0, Q4_1, Q8_0 and Q6_K M = 4..16 the band kernel of fq_mmqs.hip
+// Q4_K, Q4_0, Q4_1, Q5_K, Q8_0 and Q6_K M = 4..16 the band kernel of fq_mmqs.hip
 // (Q6_K M = 4 on wide matrices: three tokens, then the fourth); M > 32 the
 // prefill kernel
 // of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --
@@ -418,9 +418,20 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         if (rc != FQ_ERR_SHAPE) return rc;
     }
 
-    if (fq::mmqs_supported((int)dtype) && M >= (blk_band ? 3 : 4) && M <= 16 && K > 0 &&
+    // Q5_K (rows 16-byte aligned): 5..16 tokens; 4 while the bands number at
+    // most one per CU or at least eight per CU (18944 x 3584: 33.4 against
+    // 31.7 us on the fp16 MFMA path); 3 at K >= 14336 or eight bands per CU
+    // and more (3584 x 18944 54.1 -> 27.0 us at M = 4, lm_head at M = 3 166
+    // against about 150; 18944 x 3584 at M = 3 26.0 against 33)
+    const bool q5k_band =
+        dtype == FQ_DTYPE_Q5_K && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+        (M >= 5 || (M == 4 && (bands <= di.cus || bands >= 8L * di.cus)) ||
+         (M == 3 && (K >= 14336 || bands >= 8L * di.cus)));
+    if (fq::mmqs_supported((int)dtype) && M >= (blk_band || q5k_band ? 3 : 4) && M <= 16 &&
+        K > 0 &&
         (dtype == FQ_DTYPE_Q4_K   ? N <= 16 * bmt * di.cus || M > 8
          : dtype == FQ_DTYPE_Q6_K ? (reinterpret_cast<uintptr_t>(w) & 1) == 0
+         : dtype == FQ_DTYPE_Q5_K ? q5k_band
                                   : blk_band)) {
         // (Q4_0, Q8_0: see blk_band.  Q4_K beyond one band per CU only above
         // 8 tokens, which the int8 kernel does not take: 18944 x 3584 at M =

@@ -1,6 +1,6 @@
 // fq_mmqs.hip -- small-batch (M <= 16 tokens) matmul on the fp16 matrix
-// cores, streaming the GGUF rows once: Q4_K (below), and Q4_0, Q4_1, Q8_0
-// and Q6_K through their Band<> decoders further down.
+// cores, streaming the GGUF rows once: Q4_K (below), and Q4_0, Q4_1, Q5_K,
+// Q8_0 and Q6_K through their Band<> decoders further down.
 //
 // A work-group owns a band of rows, cut into TW tiles of 16; its waves split
 // the K dimension by super-blocks (super-block s goes to wave s % W), so each
@@ -83,6 +83,36 @@ struct Band<Q4_K> : BandFlags {
     // -dmin m_2g, -dmin m_2g+1
     __device__ static float4 coef4(const uint8_t* panel, int g, int r) {
         const fq_u32x4 h = *reinterpret_cast<const fq_u32x4*>(panel + 144 * r);
+        uint32_t sa, ma, sb, mb;
+        Fmt<Q4_K>::scale_min(uint4{h.x, h.y, h.z, h.w}, g, sa, ma, sb, mb);
+        const float d = f16_hw(h.x & 0xFFFFu), dmin = f16_hw(h.x >> 16);
+        return float4{d * (float)sa, d * (float)sb, -dmin * (float)ma, -dmin * (float)mb};
+    }
+};
+
+// Q5_K: the Q4_K super-block with a 32-byte plane of fifth bits (d dmin
+// scales[12] @0, qh[32] @16, qs[128] @48; 176 bytes, 16-byte aligned rows on
+// the conditions of Q4_0).  Lane (r, q) of pair g takes qs bytes 32 g + 8 q
+// .. + 7 (low nibbles: sub-block 2 g, high: 2 g + 1) and bits 2 g, 2 g + 1
+// of qh bytes 8 q .. + 7 as the codes' fifth bits (0 .. 31, exact in fp16);
+// the coefficients are those of Q4_K.
+template <>
+struct Band<Q5_K> : BandFlags {
+    static constexpr int SBK = 256, SBB = 176, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 3;
+    static constexpr bool MIN = true;
+    __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
+        const fq_u32x2 qs =
+            *reinterpret_cast<const fq_u32x2*>(panel + SBB * r + 48 + 32 * g + 8 * q);
+        const fq_u32x2 qh = *reinterpret_cast<const fq_u32x2*>(panel + SBB * r + 16 + 8 * q);
+        auto code = [&](uint32_t w, uint32_t h, int sh, int bit) {
+            return ((w >> sh) & 0x0F0F0F0Fu) | (((h >> bit) & 0x01010101u) << 4);
+        };
+        a0 = byte8(code(qs.x, qh.x, 0, 2 * g), code(qs.y, qh.y, 0, 2 * g), (_Float16)1024.0f);
+        a1 = byte8(code(qs.x, qh.x, 4, 2 * g + 1), code(qs.y, qh.y, 4, 2 * g + 1),
+                   (_Float16)1024.0f);
+    }
+    __device__ static float4 coef4(const uint8_t* panel, int g, int r) {
+        const fq_u32x4 h = *reinterpret_cast<const fq_u32x4*>(panel + SBB * r);
         uint32_t sa, ma, sb, mb;
         Fmt<Q4_K>::scale_min(uint4{h.x, h.y, h.z, h.w}, g, sa, ma, sb, mb);
         const float d = f16_hw(h.x & 0xFFFFu), dmin = f16_hw(h.x >> 16);
@@ -491,7 +521,8 @@ const void* sfn_tw(int tw, bool bias) {
 }  // namespace
 
 bool mmqs_supported(int dtype) {
-    return dtype == Q4_K || dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0 || dtype == Q6_K;
+    return dtype == Q4_K || dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0 || dtype == Q6_K ||
+           dtype == Q5_K;
 }
 
 // Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
@@ -506,13 +537,14 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int
         fn = wg == 256   ? sfn_tw<Q4_K, 256>(tw, a.bias_mode != 0)
              : wg == 1024 ? sfn_tw<Q4_K, 1024>(tw, a.bias_mode != 0)
                           : sfn_tw<Q4_K, 512>(tw, a.bias_mode != 0);
-    } else if (dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0) {
+    } else if (dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0 || dtype == Q5_K) {
         // rows must start 16-byte aligned (the panel loads are 16 bytes)
         if (a.K % 256 != 0 || a.row_bytes % 16 != 0 ||
             (reinterpret_cast<uintptr_t>(a.w) & 15) != 0 || wg != 512)
             return hipErrorInvalidValue;
         fn = dtype == Q4_0   ? sfn_tw<Q4_0, 512>(tw, a.bias_mode != 0)
              : dtype == Q4_1 ? sfn_tw<Q4_1, 512>(tw, a.bias_mode != 0)
+             : dtype == Q5_K ? sfn_tw<Q5_K, 512>(tw, a.bias_mode != 0)
                              : sfn_tw<Q8_0, 512>(tw, a.bias_mode != 0);
     } else if (dtype == Q6_K) {  // rows at even addresses (shifts of at most 14)
         if (a.K % 256 != 0 || (reinterpret_cast<uintptr_t>(a.w) & 1) != 0 || wg != 512)

@@ -226,6 +226,26 @@ def test_q6k_small_batch_band_kernel(N, K, M):
                                atol=1e-6)
 
 
+@pytest.mark.parametrize("M", [3, 4, 7, 16])
+@pytest.mark.parametrize("N,K", [(3584, 18944), (4099, 2048), (17001, 512)])
+def test_q5k_small_batch_band_kernel(N, K, M):
+    # Q5_K, 3..16 tokens (3 and 4 where the band count or K favours it), rows
+    # 16-byte aligned: the fp16 band kernel (the
+    # Q4_K panels plus the fifth-bit plane); at a 2-byte offset base the
+    # other kernels, within the same bar
+    w = synth.make_weights(F.Q5_K, N, K, seed=N + M + 11)
+    x = synth.make_x(M, K, N + M + 12)
+    y = run(F.Q5_K, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(F.Q5_K, w, min(N, 4096), K))))
+    ref = oracle.matmul_f64(F.Q5_K, x, w, N, K)
+    assert_close(y, ref, x, np.array([deq_max]), f"Q5_K M={M} {N}x{K}")
+    assert_close(run(F.Q5_K, w, x, N, K, offset=2), ref, x, np.array([deq_max]),
+                 f"Q5_K M={M} {N}x{K} offset 2")
+    b2 = torch.randn(M, N)
+    np.testing.assert_allclose(run(F.Q5_K, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
+                               atol=1e-6)
+
+
 @pytest.mark.parametrize("M", [8, 9, 16])
 def test_q4k_wide_small_batch(M):
     # Q4_K on more rows than one four-tile band per CU: the int8 kernel up to
