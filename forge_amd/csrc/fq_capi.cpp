@@ -422,12 +422,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     // most one per CU or at least eight per CU (18944 x 3584: 33.4 against
     // 31.7 us on the fp16 MFMA path); 3 at K >= 14336 or eight bands per CU
     // and more (3584 x 18944 54.1 -> 27.0 us at M = 4, lm_head at M = 3 166
-    // against about 150; 18944 x 3584 at M = 3 26.0 against 33)
+    // against about 150; 18944 x 3584 at M = 3 26.0 against 33); 2 at K >=
+    // 14336 (3584 x 18944: 53.9 on the fp16 MFMA path; lm_head at M = 2
+    // 111.5 against about 150 stays there)
     const bool q5k_band =
         dtype == FQ_DTYPE_Q5_K && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
         (M >= 5 || (M == 4 && (bands <= di.cus || bands >= 8L * di.cus)) ||
-         (M == 3 && (K >= 14336 || bands >= 8L * di.cus)));
-    if (fq::mmqs_supported((int)dtype) && M >= (blk_band || q5k_band ? 3 : 4) && M <= 16 &&
+         (M == 3 && (K >= 14336 || bands >= 8L * di.cus)) || (M == 2 && K >= 14336));
+    if (fq::mmqs_supported((int)dtype) && M >= (q5k_band ? 2 : blk_band ? 3 : 4) && M <= 16 &&
         K > 0 &&
         (dtype == FQ_DTYPE_Q4_K   ? N <= 16 * bmt * di.cus || M > 8
          : dtype == FQ_DTYPE_Q6_K ? (reinterpret_cast<uintptr_t>(w) & 1) == 0
@@ -1193,7 +1195,7 @@ int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
     for (int n = N_max; n > 0; n = n > 128 ? ((n - 1) / 128) * 128 : 0) {
         for (int m = 2; m <= M_max; ++m) {
             need0 = std::max(need0, plan_mmq(m, K_max, n, di.cus).total);
-            if (m >= 3 && m <= 16 && Kp > 0)  // band kernel, four- and two-tile bands
+            if (m <= 16 && Kp > 0)  // band kernel (from M = 2), four- and two-tile bands
                 for (int mt : {4, 2}) need0 = std::max(need0, mmqs_need(m, Kp, n, di.cus, mt));
             if (m > 32 && Kp > 0) need0 = std::max(need0, plan_mmqp(m, Kp, n, di.cus, true).total);
             // the batch-1 kernel's K-split slabs for 2..4 tokens (at most 8)

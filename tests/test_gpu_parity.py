@@ -226,10 +226,10 @@ def test_q6k_small_batch_band_kernel(N, K, M):
                                atol=1e-6)
 
 
-@pytest.mark.parametrize("M", [3, 4, 7, 16])
+@pytest.mark.parametrize("M", [2, 3, 4, 7, 16])
 @pytest.mark.parametrize("N,K", [(3584, 18944), (4099, 2048), (17001, 512)])
 def test_q5k_small_batch_band_kernel(N, K, M):
-    # Q5_K, 3..16 tokens (3 and 4 where the band count or K favours it), rows
+    # Q5_K, 2..16 tokens (2, 3 and 4 where the band count or K favours it), rows
     # 16-byte aligned: the fp16 band kernel (the
     # Q4_K panels plus the fifth-bit plane); at a 2-byte offset base the
     # other kernels, within the same bar

@@ -75,7 +75,7 @@ def test_growth_under_capture_is_refused():
                                          (F.Q6_K, 96, 2048, 1500), (F.Q4_K, 8, 18944, 3584),
                                          (F.Q6_K, 2, 18944, 3584), (F.Q4_0, 3, 18944, 3584),
                                          (F.Q6_K, 8, 18944, 3584), (F.Q8_0, 6, 18944, 3584),
-                                         (F.Q4_1, 16, 4096, 1000)])
+                                         (F.Q4_1, 16, 4096, 1000), (F.Q5_K, 2, 18944, 3584)])
 def test_reserve_then_capture_first(dtype, M, K, N):
     # fq_reserve_workspace alone (no eager call first) must cover the call's
     # kernel choice: the prefill kernel (Q8_0 / Q4_0, up to 16 K-splits; Q6_K
