@@ -6,7 +6,7 @@
 // matrices of 64k rows and more on the aligned layout, the row-step kernels
 // of fq_gemv1.hip under about 4 MB of weights); M = 2..4
 // the same batch-1 kernels with each weight unit dotted with every token;
-// Q4_K, Q4_0, Q4_1, Q5_K, Q8_0 and Q6_K M = 4..16 the band kernel of fq_mmqs.hip
+// M = 2..16 (by format and shape) the band kernel of fq_mmqs.hip
 // (Q6_K M = 4 on wide matrices: three tokens, then the fourth); M > 32 the
 // prefill kernel
 // of fq_mmqp.hip (rows in 16-byte chunks, K a multiple of 256); the rest --
@@ -425,16 +425,30 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     // against about 150; 18944 x 3584 at M = 3 26.0 against 33); 2 at K >=
     // 14336 (3584 x 18944: 53.9 on the fp16 MFMA path; lm_head at M = 2
     // 111.5 against about 150 stays there)
+    const bool al16 = K % 256 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+    // Q5_0 and IQ4_NL: K >= 14336 from 2 tokens (3584 x 18944 at M = 2..8:
+    // 55.3 -> 27.9 and 47.4 -> 28.3 us), or 4..16 tokens in one round of
+    // bands (14336 x 4096 at M = 8: 33.2 -> 21.3, 29.2 -> 21.6); 18944 rows
+    // at M = 8 measured slower (35.5 against 32.7, 36.1 against 28.4).
+    // Q5_1 (160 KB of LDS per work-group): K >= 14336 only (43.8 -> 37.5;
+    // lm_head at M = 8 216 against 159)
+    const bool q5x_band =
+        al16 && M >= 2 &&
+        (((dtype == FQ_DTYPE_Q5_0 || dtype == FQ_DTYPE_IQ4_NL) &&
+          (K >= 14336 || (M >= 4 && bands <= di.cus))) ||
+         (dtype == FQ_DTYPE_Q5_1 && K >= 14336));
     const bool q5k_band =
-        dtype == FQ_DTYPE_Q5_K && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
-        (M >= 5 || (M == 4 && (bands <= di.cus || bands >= 8L * di.cus)) ||
-         (M == 3 && (K >= 14336 || bands >= 8L * di.cus)) || (M == 2 && K >= 14336));
+        (dtype == FQ_DTYPE_Q5_K && al16 &&
+         (M >= 5 || (M == 4 && (bands <= di.cus || bands >= 8L * di.cus)) ||
+          (M == 3 && (K >= 14336 || bands >= 8L * di.cus)) || (M == 2 && K >= 14336))) ||
+        q5x_band;
     if (fq::mmqs_supported((int)dtype) && M >= (q5k_band ? 2 : blk_band ? 3 : 4) && M <= 16 &&
         K > 0 &&
         (dtype == FQ_DTYPE_Q4_K   ? N <= 16 * bmt * di.cus || M > 8
          : dtype == FQ_DTYPE_Q6_K ? (reinterpret_cast<uintptr_t>(w) & 1) == 0
-         : dtype == FQ_DTYPE_Q5_K ? q5k_band
-                                  : blk_band)) {
+         : (dtype == FQ_DTYPE_Q4_0 || dtype == FQ_DTYPE_Q4_1 || dtype == FQ_DTYPE_Q8_0)
+             ? blk_band
+             : q5k_band)) {
         // (Q4_0, Q8_0: see blk_band.  Q4_K beyond one band per CU only above
         // 8 tokens, which the int8 kernel does not take: 18944 x 3584 at M =
         // 16 31.2 against 34.4 us on the fp16 MFMA path, 152064 x 3584 143.5

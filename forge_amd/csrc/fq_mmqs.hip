@@ -1,6 +1,7 @@
 // fq_mmqs.hip -- small-batch (M <= 16 tokens) matmul on the fp16 matrix
-// cores, streaming the GGUF rows once: Q4_K (below), and Q4_0, Q4_1, Q5_K,
-// Q8_0 and Q6_K through their Band<> decoders further down.
+// cores, streaming the GGUF rows once: Q4_K (below), and Q4_0, Q4_1, Q5_0,
+// Q5_1, Q5_K, IQ4_NL, Q8_0 and Q6_K through their Band<> decoders further
+// down.
 //
 // A work-group owns a band of rows, cut into TW tiles of 16; its waves split
 // the K dimension by super-blocks (super-block s goes to wave s % W), so each
@@ -250,6 +251,53 @@ struct Band<Q6_K> {
                       d * (float)(int8_t)((sc >> 16) & 0xFF), d * (float)(int8_t)(sc >> 24)};
     }
 };
+
+// Q5_0 (22-byte blocks: d | qh u32 | qs[16]), Q5_1 (24: d m | qh | qs) and
+// IQ4_NL (18: d | qs, a 16-entry int8 table): eight blocks are 176 / 192 /
+// 144 bytes per 256 elements and row (16-byte aligned on the conditions of
+// Q4_0).  Lane (r, q) takes elements 8 q .. 8 q + 7 of blocks 2 g and 2 g + 1:
+// the low (q < 2) or high nibbles of qs bytes 8 (q & 1) .. + 7 with, for the
+// 5-bit formats, bits 8 q .. 8 q + 7 of qh as the fifth bits; Q5_0 enters as
+// q - 16, Q5_1 as q with m on the sub-block sums, IQ4_NL as its table value.
+template <int F>
+struct BandSmall : BandFlags {
+    static constexpr int BB = F == Q5_0 ? 22 : F == Q5_1 ? 24 : 18;
+    static constexpr int SBK = 256, SBB = 8 * BB, PANEL = 16 * SBB, PIECES = PANEL / 16, NPL = 3;
+    static constexpr bool MIN = F == Q5_1;
+    static constexpr int QS = F == Q5_0 ? 6 : F == Q5_1 ? 8 : 2, QH = F == Q5_1 ? 4 : 2;
+    // the block's eight codes as an h8 (o: the block's offset in the panel)
+    template <int OFF>
+    __device__ static h8 block(const uint8_t* panel, int o, int q) {
+        const int oq = o + QS + 8 * (q & 1), sh = q < 2 ? 0 : 4;
+        const fq_u32x2 b = (OFF + QS) % 4 == 2 ? pan_ld8<true>(panel, oq) : pan_ld8<false>(panel, oq);
+        uint32_t w0 = (b.x >> sh) & 0x0F0F0F0Fu, w1 = (b.y >> sh) & 0x0F0F0F0Fu;
+        if constexpr (F == IQ4_NL) {
+            return byte8(iq4_lookup(w0) ^ 0x80808080u, iq4_lookup(w1) ^ 0x80808080u,
+                         (_Float16)1152.0f);
+        } else {
+            const uint32_t qh = pan_ld4(panel, o + QH) >> (8 * q);
+            return byte8(five_bit(w0, qh), five_bit(w1, qh >> 4),
+                         (_Float16)(F == Q5_0 ? 1040.0f : 1024.0f));
+        }
+    }
+    __device__ static void operands(const uint8_t* panel, int g, int r, int q, h8& a0, h8& a1) {
+        const int o = SBB * r + 2 * BB * g;  // block 2 g (SBB r and 2 BB g are multiples of 4)
+        a0 = block<0>(panel, o, q);
+        a1 = block<BB>(panel, o + BB, q);
+    }
+    __device__ static float4 coef4(const uint8_t* panel, int g, int r) {
+        const int o = SBB * r + 2 * BB * g;
+        const uint32_t h0 = pan_ld4(panel, o), h1 = pan_ld4(panel, o + BB);
+        return float4{f16_hw(h0 & 0xFFFFu), f16_hw(h1 & 0xFFFFu),
+                      MIN ? f16_hw(h0 >> 16) : 0.0f, MIN ? f16_hw(h1 >> 16) : 0.0f};
+    }
+};
+template <>
+struct Band<Q5_0> : BandSmall<Q5_0> {};
+template <>
+struct Band<Q5_1> : BandSmall<Q5_1> {};
+template <>
+struct Band<IQ4_NL> : BandSmall<IQ4_NL> {};
 
 template <int F, int TW, int WG, bool BIAS>
 __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, int sb_per_split) {
@@ -522,7 +570,7 @@ const void* sfn_tw(int tw, bool bias) {
 
 bool mmqs_supported(int dtype) {
     return dtype == Q4_K || dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0 || dtype == Q6_K ||
-           dtype == Q5_K;
+           dtype == Q5_K || dtype == Q5_0 || dtype == Q5_1 || dtype == IQ4_NL;
 }
 
 // Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
@@ -537,7 +585,8 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int
         fn = wg == 256   ? sfn_tw<Q4_K, 256>(tw, a.bias_mode != 0)
              : wg == 1024 ? sfn_tw<Q4_K, 1024>(tw, a.bias_mode != 0)
                           : sfn_tw<Q4_K, 512>(tw, a.bias_mode != 0);
-    } else if (dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0 || dtype == Q5_K) {
+    } else if (dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0 || dtype == Q5_K ||
+               dtype == Q5_0 || dtype == Q5_1 || dtype == IQ4_NL) {
         // rows must start 16-byte aligned (the panel loads are 16 bytes)
         if (a.K % 256 != 0 || a.row_bytes % 16 != 0 ||
             (reinterpret_cast<uintptr_t>(a.w) & 15) != 0 || wg != 512)
@@ -545,6 +594,9 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int
         fn = dtype == Q4_0   ? sfn_tw<Q4_0, 512>(tw, a.bias_mode != 0)
              : dtype == Q4_1 ? sfn_tw<Q4_1, 512>(tw, a.bias_mode != 0)
              : dtype == Q5_K ? sfn_tw<Q5_K, 512>(tw, a.bias_mode != 0)
+             : dtype == Q5_0 ? sfn_tw<Q5_0, 512>(tw, a.bias_mode != 0)
+             : dtype == Q5_1 ? sfn_tw<Q5_1, 512>(tw, a.bias_mode != 0)
+             : dtype == IQ4_NL ? sfn_tw<IQ4_NL, 512>(tw, a.bias_mode != 0)
                              : sfn_tw<Q8_0, 512>(tw, a.bias_mode != 0);
     } else if (dtype == Q6_K) {  // rows at even addresses (shifts of at most 14)
         if (a.K % 256 != 0 || (reinterpret_cast<uintptr_t>(a.w) & 1) != 0 || wg != 512)

@@ -228,21 +228,24 @@ def test_q6k_small_batch_band_kernel(N, K, M):
 
 @pytest.mark.parametrize("M", [2, 3, 4, 7, 16])
 @pytest.mark.parametrize("N,K", [(3584, 18944), (4099, 2048), (17001, 512)])
-def test_q5k_small_batch_band_kernel(N, K, M):
-    # Q5_K, 2..16 tokens (2, 3 and 4 where the band count or K favours it), rows
-    # 16-byte aligned: the fp16 band kernel (the
-    # Q4_K panels plus the fifth-bit plane); at a 2-byte offset base the
-    # other kernels, within the same bar
-    w = synth.make_weights(F.Q5_K, N, K, seed=N + M + 11)
+@pytest.mark.parametrize("dtype", [F.Q5_K, F.Q5_0, F.Q5_1, F.IQ4_NL])
+def test_q5k_small_batch_band_kernel(dtype, N, K, M):
+    # Q5_K, Q5_0, Q5_1 and IQ4_NL at 2..16 tokens, rows 16-byte aligned: the
+    # fp16 band kernel where the format's rule takes it (Q5_K: the Q4_K
+    # panels plus the fifth-bit plane; the others eight blocks per panel row;
+    # long K for all, one round of bands for Q5_K, Q5_0, IQ4_NL), the other
+    # kernels elsewhere and at a 2-byte offset base, all within the same bar
+    name = F.fmt(dtype).name
+    w = synth.make_weights(dtype, N, K, seed=N + M + 11)
     x = synth.make_x(M, K, N + M + 12)
-    y = run(F.Q5_K, w, x, N, K)
-    deq_max = float(np.max(np.abs(oracle.dequant(F.Q5_K, w, min(N, 4096), K))))
-    ref = oracle.matmul_f64(F.Q5_K, x, w, N, K)
-    assert_close(y, ref, x, np.array([deq_max]), f"Q5_K M={M} {N}x{K}")
-    assert_close(run(F.Q5_K, w, x, N, K, offset=2), ref, x, np.array([deq_max]),
-                 f"Q5_K M={M} {N}x{K} offset 2")
+    y = run(dtype, w, x, N, K)
+    deq_max = float(np.max(np.abs(oracle.dequant(dtype, w, min(N, 4096), K))))
+    ref = oracle.matmul_f64(dtype, x, w, N, K)
+    assert_close(y, ref, x, np.array([deq_max]), f"{name} M={M} {N}x{K}")
+    assert_close(run(dtype, w, x, N, K, offset=2), ref, x, np.array([deq_max]),
+                 f"{name} M={M} {N}x{K} offset 2")
     b2 = torch.randn(M, N)
-    np.testing.assert_allclose(run(F.Q5_K, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
+    np.testing.assert_allclose(run(dtype, w, x, N, K, bias=b2), y + b2.numpy(), rtol=1e-6,
                                atol=1e-6)
 
 
