@@ -547,10 +547,10 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
 
     if (fq::mmqi_supported((int)dtype) && M >= 3 && M <= 8 && K > 0) {
         // Q4_K, 3..8 tokens that the kernels above do not take: three tokens
-        // on weights under 8 MB or rows whose three record sets overflow the
-        // batch-1 kernel's LDS (K = 18944), and 4..8 tokens on more rows than
-        // one mmqs band per CU covers.  The int8 matrix-core kernel runs them
-        // in one pass (M > 8 goes to the fp16 MFMA path)
+        // on weights under 8 MB (from 8 MB the batch-1 kernel takes them, with
+        // K split where the records overflow its LDS), and 4..8 tokens on more
+        // rows than one mmqs band per CU covers.  The int8 matrix-core kernel
+        // runs them in one pass (M = 9..16 takes the band kernel above)
         const long T = (N + 15) / 16;
         const long G = std::max(1L, std::min<long>(di.cus, T));
         const int tpw = (int)((T + G - 1) / G);
