@@ -454,12 +454,12 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         // 16 31.2 against 34.4 us on the fp16 MFMA path, 152064 x 3584 143.5
         // against 170.4; at M = 4..8 the int8 kernel is faster, 21.1-27.5
         // against 30.2-30.4 and 108-130 against 137-139)
-        // 4..16 tokens: token operands, then one pass over the weights on the
-        // fp16 matrix cores, one band of rows per work-group (measured at
-        // 14336 x 4096: 19.2-19.7 us for every M in 4..16, against 21-30 us on
-        // the int8 matrix-core and fp16 MFMA paths; M = 2, 3 are faster on the
-        // row-step and int8 kernels, and rows beyond one band per CU on the
-        // int8 kernel)
+        // 2..16 tokens (by format and shape, above): token operands, then one
+        // pass over the weights on the fp16 matrix cores, one band of rows per
+        // work-group (Q4_K at 14336 x 4096: 19.2-19.7 us for every M in 4..16,
+        // against 21-30 us on the int8 matrix-core and fp16 MFMA paths; Q4_K
+        // at M = 2, 3 is faster on the batch-1 and int8 kernels, and at M =
+        // 4..8 on rows beyond one band per CU on the int8 kernel)
         const int NC = K / 64;
         const MmqPlan pl = plan_mmq(M, K, N, di.cus);
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
