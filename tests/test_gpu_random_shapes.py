@@ -77,3 +77,37 @@ def test_random_shape(dt, M, N, K, seed, r):
         y64 = y64 + bias.numpy().astype(np.float64)
     deq = float(np.max(np.abs(oracle.dequant(dt, w, N, K))))
     assert_close(y, y64, x, np.array([deq]), f"{F.fmt(dt).name} M={M} N={N} K={K}")
+
+
+def _small_batch_cases():
+    rng = np.random.default_rng(20261203)
+    out = []
+    allf = sorted(F.FORMATS)
+    while len(out) < 80:
+        dt = int(rng.choice(allf))
+        be = F.fmt(dt).block_elems
+        M = int(rng.choice([2, 3, 4, 5, 6, 8, 9, 12, 16]))
+        N = int(rng.choice([int(rng.integers(1, 3000)), int(rng.integers(3000, 20000))]))
+        K = (256 * int(rng.integers(1, 75)) if rng.random() < 0.8
+             else be * int(rng.integers(1, 19000 // be)))
+        if M * N * K > 4e8 or N * K > 1.2e8:
+            continue
+        out.append((dt, M, N, K, int(rng.integers(1 << 30)), float(rng.random()),
+                    int(rng.choice([0, 0, 2, 16]))))
+    return out
+
+
+@pytest.mark.parametrize("dt,M,N,K,seed,r,off", _small_batch_cases())
+def test_random_small_batch(dt, M, N, K, seed, r, off):
+    from test_gpu_parity import dev_weight
+    w = synth.make_weights(dt, N, K, seed=seed)
+    x = synth.make_x(M, K, seed=seed + 1)
+    bias = torch.from_numpy(synth.make_x(1, N, seed + 2).reshape(N)) if r < 0.3 else None
+    y = ops.matmul_transB(torch.from_numpy(x).cuda(), dev_weight(dt, w, N, K, off),
+                          bias.cuda() if bias is not None else None).cpu().numpy()
+    y64 = oracle.matmul_f64(dt, x, w, N, K)
+    if bias is not None:
+        y64 = y64 + bias.numpy().astype(np.float64)
+    deq = float(np.max(np.abs(oracle.dequant(dt, w, min(N, 4096), K))))
+    assert_close(y, y64, x, np.array([deq]),
+                 f"{F.fmt(dt).name} M={M} N={N} K={K} offset {off}")
