@@ -437,8 +437,14 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         (((dtype == FQ_DTYPE_Q5_0 || dtype == FQ_DTYPE_IQ4_NL) &&
           (K >= 14336 || (M >= 4 && bands <= di.cus))) ||
          (dtype == FQ_DTYPE_Q5_1 && K >= 14336));
+    // Q3_K (rows at even addresses): K >= 14336 from two tokens (3584 x 18944
+    // 61 -> 28.7 us), 4..16 tokens for any row count (152064 x 3584 at M = 8
+    // 262 -> 184, 14336 x 4096 41.9 -> 32.0; equal at M = 4)
+    const bool q3k_band = dtype == FQ_DTYPE_Q3_K && K % 256 == 0 &&
+                          (reinterpret_cast<uintptr_t>(w) & 1) == 0 && M >= 2 &&
+                          (K >= 14336 || M >= 4);
     const bool q5k_band =
-        (dtype == FQ_DTYPE_Q5_K && al16 &&
+        q3k_band || (dtype == FQ_DTYPE_Q5_K && al16 &&
          (M >= 5 || (M == 4 && (bands <= di.cus || bands >= 8L * di.cus)) ||
           (M == 3 && (K >= 14336 || bands >= 8L * di.cus)) || (M == 2 && K >= 14336))) ||
         q5x_band;

@@ -1,7 +1,7 @@
 // fq_mmqs.hip -- small-batch (M <= 16 tokens) matmul on the fp16 matrix
 // cores, streaming the GGUF rows once: Q4_K (below), and Q4_0, Q4_1, Q5_0,
-// Q5_1, Q5_K, IQ4_NL, Q8_0 and Q6_K through their Band<> decoders further
-// down.
+// Q5_1, Q5_K, IQ4_NL, Q8_0, Q6_K and Q3_K through their Band<> decoders
+// further down.
 //
 // A work-group owns a band of rows, cut into TW tiles of 16; its waves split
 // the K dimension by super-blocks (super-block s goes to wave s % W), so each
@@ -299,6 +299,54 @@ struct Band<Q5_1> : BandSmall<Q5_1> {};
 template <>
 struct Band<IQ4_NL> : BandSmall<IQ4_NL> {};
 
+// Q3_K: 110-byte super-blocks (hmask[32] | qs[64] | scales[12] | d), rows
+// 2-byte aligned: loaded from the aligned-down start like Q6_K, at most
+// eight pieces (a panel row of 128 bytes; only pieces that start before the
+// row's end are loaded).  Element e, n = e / 128, plane j = (e % 128) / 32,
+// l = e % 32: bits 2 j .. 2 j + 1 of qs[32 n + l] and bit 4 n + j of
+// hmask[l] make the code c = q2 + 4 h, weight d (sc[e / 16] - 32) (c - 4).
+// Chunk g: n = g / 2, sub-block s takes plane 2 (g & 1) + s / 2 and l = 16
+// (s & 1) + 4 q + 0 .. 3 for lane (r, q), as c - 4 (1024 + c - 1028).
+// Sub-block scale i (6 bits): the low four in nibble i / 8 of scales[i % 8],
+// the top two at bit 2 (i / 4) of scales[8 + i % 4].
+template <>
+struct Band<Q3_K> {
+    static constexpr bool SB16 = true, SHIFT = true, MIN = false;
+    static constexpr int SBK = 256, SBB = 110, PANEL = 16 * 128, PIECES = PANEL / 16, NPL = 2;
+    __device__ static void operands(const uint8_t* panel, int ro, int g, int q, h4 (&a)[4]) {
+        const int n = g >> 1, jb = 2 * (g & 1);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint32_t hm = pan_ld4(panel, ro + 16 * hf + 4 * q);
+            const uint32_t qs = pan_ld4(panel, ro + 32 + 32 * n + 16 * hf + 4 * q);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int j = jb + jj;
+                const uint32_t v = ((qs >> (2 * j)) & 0x03030303u) |
+                                   (((hm >> (4 * n + j)) & 0x01010101u) << 2);
+                h2 p0, p1;
+                byte_pairs(v, (_Float16)1028.0f, p0, p1);
+                a[2 * jj + hf] = h4{p0[0], p0[1], p1[0], p1[1]};
+            }
+        }
+    }
+    // d (sc - 32) of the chunk's four sub-blocks i = 4 g .. 4 g + 3
+    __device__ static float4 coef4(const uint8_t* panel, int ro, int g) {
+        const uint32_t lo = pan_ld4(panel, ro + 96 + 4 * (g & 1));  // scales[i % 8], 4 of them
+        const uint32_t hi = pan_ld4(panel, ro + 104);               // scales[8 .. 11]
+        const float d = f16_hw(pan_ld4(panel, ro + 108) & 0xFFFFu);
+        float c[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int i = 4 * g + s;
+            const uint32_t l4 = (lo >> (8 * s + 4 * (i >> 3))) & 15u;
+            const uint32_t h2b = (hi >> (8 * (i & 3) + 2 * (i >> 2))) & 3u;
+            c[s] = d * (float)((int)(l4 | (h2b << 4)) - 32);
+        }
+        return float4{c[0], c[1], c[2], c[3]};
+    }
+};
+
 template <int F, int TW, int WG, bool BIAS>
 __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, int sb_per_split) {
     using B = Band<F>;
@@ -345,9 +393,20 @@ __global__ __launch_bounds__(WG) void mmqs_kernel(MmqArgs a, int rows_per_wg, in
             for (int i = 0; i < NPL; ++i) {
                 const int rr = min(pp[i] / PPR, rmax[t]);  // rows past N repeat the last
                 const uint8_t* rs = prow[t] + (size_t)rr * a.row_bytes + B::SBB * sb;
-                if constexpr (B::SHIFT) rs -= reinterpret_cast<uintptr_t>(rs) & 15;
-                const uint8_t* p = rs + 16 * (pp[i] - PPR * (pp[i] / PPR));
-                pv[t][i] = __builtin_nontemporal_load(reinterpret_cast<const fq_u32x4*>(p));
+                const int pj = pp[i] - PPR * (pp[i] / PPR);  // piece of the panel row
+                if constexpr (B::SHIFT) {
+                    // from the aligned-down start; pieces wholly past the
+                    // row's end are not loaded (they could leave its page)
+                    const int sh = (int)(reinterpret_cast<uintptr_t>(rs) & 15);
+                    rs -= sh;
+                    pv[t][i] = fq_u32x4{0u, 0u, 0u, 0u};
+                    if (16 * pj < sh + B::SBB)
+                        pv[t][i] = __builtin_nontemporal_load(
+                            reinterpret_cast<const fq_u32x4*>(rs + 16 * pj));
+                } else {
+                    pv[t][i] = __builtin_nontemporal_load(
+                        reinterpret_cast<const fq_u32x4*>(rs + 16 * pj));
+                }
             }
     };
 
@@ -557,7 +616,8 @@ const void* sfn_tw(int tw, bool bias) {
         case 1: return sfn<F, 1, WG>(bias);
         case 2: return sfn<F, 2, WG>(bias);
     }
-    if constexpr (WG <= 512 && F != Q8_0 && F != Q6_K) {  // Q8_0, Q6_K: two tiles (LDS)
+    // Q8_0, Q6_K: two tiles (LDS); Q3_K: two (four spill)
+    if constexpr (WG <= 512 && F != Q8_0 && F != Q6_K && F != Q3_K) {
         switch (tw) {
             case 3: return sfn<F, 3, WG>(bias);
             case 4: return sfn<F, 4, WG>(bias);
@@ -570,12 +630,14 @@ const void* sfn_tw(int tw, bool bias) {
 
 bool mmqs_supported(int dtype) {
     return dtype == Q4_K || dtype == Q4_0 || dtype == Q4_1 || dtype == Q8_0 || dtype == Q6_K ||
-           dtype == Q5_K || dtype == Q5_0 || dtype == Q5_1 || dtype == IQ4_NL;
+           dtype == Q5_K || dtype == Q5_0 || dtype == Q5_1 || dtype == IQ4_NL || dtype == Q3_K;
 }
 
 // Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
-// rows): Q8_0's 272-byte panels fit two per wave in LDS at 512 threads.
-int mmqs_max_tiles(int dtype) { return dtype == Q8_0 || dtype == Q6_K ? 2 : 4; }
+// rows): Q8_0's 272-byte panels fit two per wave in LDS at 512 threads;
+// Q6_K and Q3_K take two (their 16-element sub-blocks need twice the
+// operand registers per tile).
+int mmqs_max_tiles(int dtype) { return dtype == Q8_0 || dtype == Q6_K || dtype == Q3_K ? 2 : 4; }
 
 hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int splits,
                        hipStream_t st) {
@@ -598,10 +660,11 @@ hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int
              : dtype == Q5_1 ? sfn_tw<Q5_1, 512>(tw, a.bias_mode != 0)
              : dtype == IQ4_NL ? sfn_tw<IQ4_NL, 512>(tw, a.bias_mode != 0)
                              : sfn_tw<Q8_0, 512>(tw, a.bias_mode != 0);
-    } else if (dtype == Q6_K) {  // rows at even addresses (shifts of at most 14)
+    } else if (dtype == Q6_K || dtype == Q3_K) {  // rows at even addresses (shifts <= 14)
         if (a.K % 256 != 0 || (reinterpret_cast<uintptr_t>(a.w) & 1) != 0 || wg != 512)
             return hipErrorInvalidValue;
-        fn = sfn_tw<Q6_K, 512>(tw, a.bias_mode != 0);
+        fn = dtype == Q6_K ? sfn_tw<Q6_K, 512>(tw, a.bias_mode != 0)
+                           : sfn_tw<Q3_K, 512>(tw, a.bias_mode != 0);
     }
     if (!fn) return hipErrorInvalidValue;
     const int nsb = a.K / 256;

@@ -228,13 +228,15 @@ def test_q6k_small_batch_band_kernel(N, K, M):
 
 @pytest.mark.parametrize("M", [2, 3, 4, 7, 16])
 @pytest.mark.parametrize("N,K", [(3584, 18944), (4099, 2048), (17001, 512)])
-@pytest.mark.parametrize("dtype", [F.Q5_K, F.Q5_0, F.Q5_1, F.IQ4_NL])
+@pytest.mark.parametrize("dtype", [F.Q5_K, F.Q5_0, F.Q5_1, F.IQ4_NL, F.Q3_K])
 def test_q5k_small_batch_band_kernel(dtype, N, K, M):
-    # Q5_K, Q5_0, Q5_1 and IQ4_NL at 2..16 tokens, rows 16-byte aligned: the
-    # fp16 band kernel where the format's rule takes it (Q5_K: the Q4_K
-    # panels plus the fifth-bit plane; the others eight blocks per panel row;
-    # long K for all, one round of bands for Q5_K, Q5_0, IQ4_NL), the other
-    # kernels elsewhere and at a 2-byte offset base, all within the same bar
+    # Q5_K, Q5_0, Q5_1, IQ4_NL and Q3_K at 2..16 tokens: the fp16 band kernel
+    # where the format's rule takes it (Q5_K: the Q4_K panels plus the
+    # fifth-bit plane; Q5_0, Q5_1, IQ4_NL eight blocks per panel row, rows
+    # 16-byte aligned; Q3_K rows read at their byte shift; long K for all,
+    # one round of bands for Q5_K, Q5_0, IQ4_NL, Q3_K), the other kernels
+    # elsewhere and, except Q3_K, at a 2-byte offset base; all within the
+    # same bar
     name = F.fmt(dtype).name
     w = synth.make_weights(dtype, N, K, seed=N + M + 11)
     x = synth.make_x(M, K, N + M + 12)
