@@ -294,9 +294,14 @@ int run_mmq(uint32_t dtype, const Geometry& g, const float* x, const void* w, co
     return e == hipSuccess ? FQ_OK : hip_fail(e);
 }
 
+// band_x (optional): in, true when the stream's slot-0 workspace already
+// holds the band kernel's token operands of this x, M, K and format (a call
+// just before with the same x, M, K, N and format took the band kernel:
+// same plan, same workspace size, so the buffer was not replaced); out,
+// whether this call took the band kernel.
 int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias, int bias_mode,
                int64_t bias_len, float* y, int M, int K, int N, hipStream_t st,
-               uint8_t* fixed = nullptr, size_t fixed_cap = 0);
+               uint8_t* fixed = nullptr, size_t fixed_cap = 0, bool* band_x = nullptr);
 
 // Fixed workspace of fq_matmul_transB_noalloc, for callers that cannot
 // allocate (HIP-graph capture, serving loops that forbid hipMalloc).  Every
@@ -331,7 +336,9 @@ int packed_gemv(uint32_t dtype, const float* x, const void* w_packed, const void
 
 int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias, int bias_mode,
                int64_t bias_len, float* y, int M, int K, int N, hipStream_t st, uint8_t* fixed,
-               size_t fixed_cap) {
+               size_t fixed_cap, bool* band_x) {
+    const bool x_ready = band_x && *band_x;
+    if (band_x) *band_x = false;
     Geometry g;
     if (!geometry(dtype, g)) return FQ_ERR_DTYPE;
     if (M < 0 || N < 0 || K < 0) return FQ_ERR_SHAPE;
@@ -498,11 +505,15 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         a.K = K;
         a.NC = NC;
         a.row_bytes = (K / g.be) * g.bb;
-        e = fq::launch_xprep((int)dtype, x, M, K, NC, reinterpret_cast<_Float16*>(buf),
-                             const_cast<float*>(a.xsum), const_cast<int*>(a.ex), st);
-        if (e != hipSuccess) return hip_fail(e);
+        if (!x_ready) {
+            e = fq::launch_xprep((int)dtype, x, M, K, NC, reinterpret_cast<_Float16*>(buf),
+                                 const_cast<float*>(a.xsum), const_cast<int*>(a.ex), st);
+            if (e != hipSuccess) return hip_fail(e);
+        }
         e = fq::launch_mmqs((int)dtype, a, rpw, 512, splits, st);
-        return e == hipSuccess ? FQ_OK : hip_fail(e);
+        if (e != hipSuccess) return hip_fail(e);
+        if (band_x) *band_x = true;
+        return FQ_OK;
     }
 
     if ((M == 1 || M == 2) && K > 0) {
@@ -1191,9 +1202,13 @@ int fq_ffn_up_fused(uint32_t dtype, const float* x, const void* w_gate, const vo
     if (rs != FQ_OK) return rs;
     float* gate = reinterpret_cast<float*>(buf);
     float* up = gate + (size_t)M * N;
-    int rc = run_matmul(dtype, x, w_gate, nullptr, 0, 0, gate, M, K, N, st);
+    // gate and up share x, M, K, N and the format: when the gate call takes
+    // the band kernel, the up call does too and reuses its token operands
+    // (one token-prep launch fewer: about 5 us)
+    bool band_x = false;
+    int rc = run_matmul(dtype, x, w_gate, nullptr, 0, 0, gate, M, K, N, st, nullptr, 0, &band_x);
     if (rc != FQ_OK) return rc;
-    rc = run_matmul(dtype, x, w_up, nullptr, 0, 0, up, M, K, N, st);
+    rc = run_matmul(dtype, x, w_up, nullptr, 0, 0, up, M, K, N, st, nullptr, 0, &band_x);
     if (rc != FQ_OK) return rc;
     e = fq::launch_silu_mul(gate, up, y, (size_t)M * N, di.cus, st);
     return e == hipSuccess ? FQ_OK : hip_fail(e);

@@ -109,6 +109,27 @@ def test_fused_gguf_one_launch(name, dtype, N, K):
     assert torch.equal(y, ops.ffn_up_fused(xd, Wg, Wu)), "fused GGUF GEMV is not deterministic"
 
 
+@pytest.mark.parametrize("dtype,N,K,M,off", [(F.Q4_K, 4096, 4096, 8, 0), (F.Q4_0, 1000, 4096, 5, 0),
+                                              (F.Q4_0, 1000, 4096, 5, 2), (F.Q6_K, 700, 4352, 9, 0),
+                                              (F.Q8_0, 2000, 2048, 16, 0)])
+def test_ffn_up_small_batch_shared_operands(dtype, N, K, M, off):
+    # 2..16 tokens: gate and up as two matmuls; when both take the band
+    # kernel the up call reuses the gate call's token operands (off = 2: the
+    # up matrix at a 2-byte offset takes another kernel and prepares its
+    # own).  The same as the two matmuls with silu(g) * u in torch (only
+    # the SiLU implementations differ, within 1e-5)
+    wg, wu = make(dtype, N, K, 71)
+    x = synth.make_x(M, K, seed=72)
+    xd = torch.from_numpy(x).cuda()
+    Wg, Wu = dev_weight(dtype, wg, N, K), dev_weight(dtype, wu, N, K, off)
+    y = ops.ffn_up_fused(xd, Wg, Wu)
+    check(y.cpu().numpy(), dtype, x, wg, wu, N, K, f"{F.fmt(dtype).name} M={M} off={off}")
+    g = ops.matmul_transB(xd, Wg)
+    u = ops.matmul_transB(xd, Wu)
+    ref = torch.nn.functional.silu(g) * u
+    torch.testing.assert_close(y, ref, rtol=1e-5, atol=1e-6)
+
+
 def test_fused_q4k_unaligned_base():
     # the fused forms on Q4_K GGUF rows with one matrix at a 2-byte offset
     # from an aligned allocation: each matrix's K-slices are staged from the
