@@ -1149,10 +1149,28 @@ int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk,
     const int rs = lease.get((size_t)M * nmax * sizeof(float), st, &buf);
     if (rs != FQ_OK) return rs;
     float* tmp = reinterpret_cast<float*>(buf);
+    // The band kernel's token operands serve every matmul here that takes
+    // it, one after another: the stream's slot-0 workspace is first grown to
+    // the largest of their band-kernel needs, so none of these calls replaces
+    // it (a call on another path clears the flag, and the next band call
+    // prepares again).  Where that growth is refused (graph capture with a
+    // smaller reserve) each call prepares its own.
+    bool share = false;
+    if (M <= 16 && K % 256 == 0) {
+        size_t need = 0;
+        for (int i = 0; i < 3; ++i)
+            if (ns[i] > 0)
+                for (int mt : {4, 2}) need = std::max(need, mmqs_need(M, K, ns[i], di.cus, mt));
+        StreamScratch::Lease l0(stream_scratch(dev, st, 0));
+        uint8_t* p0 = nullptr;
+        share = l0.get(need, st, &p0) == FQ_OK;
+    }
+    bool band_x = false;
     int off = 0;
     for (int i = 0; i < 3; ++i) {
         if (ns[i] > 0) {
-            const int rc = run_matmul(dtype, x, ws[i], nullptr, 0, 0, tmp, M, K, ns[i], st);
+            const int rc = run_matmul(dtype, x, ws[i], nullptr, 0, 0, tmp, M, K, ns[i], st,
+                                      nullptr, 0, share ? &band_x : nullptr);
             if (rc != FQ_OK) return rc;
             e = fq::launch_copy_cols(tmp, y, M, ns[i], Nt, off, di.cus, st);
             if (e != hipSuccess) return hip_fail(e);

@@ -130,6 +130,26 @@ def test_ffn_up_small_batch_shared_operands(dtype, N, K, M, off):
     torch.testing.assert_close(y, ref, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype,K,ns,M,off", [(F.Q4_K, 4096, (4096, 1024, 1024), 8, 0),
+                                              (F.Q4_0, 4096, (2048, 512, 512), 6, 2),
+                                              (F.Q6_K, 3584, (3584, 512, 512), 12, 0),
+                                              (F.Q5_K, 18944, (700, 300, 300), 3, 0)])
+def test_fused_qkv_small_batch_shared_operands(dtype, K, ns, M, off):
+    # 2..16 tokens: three matmuls; those that take the band kernel reuse one
+    # token-operand preparation (off = 2: K at a 2-byte offset base takes
+    # another kernel between Q and V, and V prepares again).  Bit-identical
+    # to the three matmuls run apart
+    ws = [synth.make_weights(dtype, n, K, 80 + i) for i, n in enumerate(ns)]
+    x = synth.make_x(M, K, seed=85)
+    xd = torch.from_numpy(x).cuda()
+    Ws = [dev_weight(dtype, w, n, K, off if i == 1 else 0) for i, (w, n) in enumerate(zip(ws, ns))]
+    y = ops.fused_qkv(xd, *Ws)
+    ref = torch.cat([ops.matmul_transB(xd, W) for W in Ws], dim=1)
+    assert torch.equal(y, ref)
+    y64 = np.concatenate([oracle.matmul_f64(dtype, x, w, n, K) for w, n in zip(ws, ns)], axis=1)
+    assert_matmul(y.cpu().numpy(), y64, x, ws, dtype, K, f"{F.fmt(dtype).name} M={M}")
+
+
 def test_fused_q4k_unaligned_base():
     # the fused forms on Q4_K GGUF rows with one matrix at a 2-byte offset
     # from an aligned allocation: each matrix's K-slices are staged from the

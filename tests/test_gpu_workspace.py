@@ -113,3 +113,35 @@ def test_reserve_then_capture_first(dtype, M, K, N):
         torch.cuda.synchronize()
     del g
     assert L.fq_release_workspace(side.cuda_stream) == 0
+
+
+def test_fused_qkv_small_batch_graph_replays():
+    # fused QKV at 8 tokens under capture after fq_reserve_workspace: the
+    # band kernel's shared token operands need slot 0 at its largest band
+    # size, which the reserve covers; every replay equals the eager call
+    from forge_amd import ops
+    L = _lib.lib()
+    dtype, M, K, ns = F.Q4_K, 8, 4096, (4096, 1024, 1024)
+    Ws = [ops.QWeight.from_numpy(synth.make_weights(dtype, n, K, 90 + i), dtype, n, K,
+                                 device="cuda") for i, n in enumerate(ns)]
+    x = torch.from_numpy(synth.make_x(M, K, 95)).cuda()
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    assert L.fq_reserve_workspace(M, K, max(ns), side.cuda_stream) == 0
+    with torch.cuda.stream(side):
+        ref = ops.fused_qkv(x, *Ws).clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        y = ops.fused_qkv(x, *Ws)
+    for _ in range(3):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref)
+        with torch.cuda.stream(side):
+            ops.fused_qkv(x * 2, *Ws)
+        torch.cuda.synchronize()
+    del g
+    assert L.fq_release_workspace(side.cuda_stream) == 0
