@@ -476,9 +476,24 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         const int NC = K / 64;
         const MmqPlan pl = plan_mmq(M, K, N, di.cus);
         auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+        // Q8_0: two- or three-tile bands, whichever the estimate (rounds of
+        // work-groups x tiles x super-blocks per split) puts lower, three
+        // within 5 % (14336 x 4096 at M = 8: 24.2 us on two, 30.1 on three;
+        // 152064 x 3584: 175.4 / 170.0; 18944 x 3584: 31.3 / 29.6)
+        int tiles = bmt;
+        if (dtype == FQ_DTYPE_Q8_0) {
+            auto est = [&](int mt) {
+                int r = 0;
+                const long sp = mmqs_plan(N, K, di.cus, &r, mt);
+                const long wgs = ((long)N + r - 1) / r * sp;
+                return (double)((wgs + di.cus - 1) / di.cus) * (r / 16) *
+                       (double)((K / 256 + sp - 1) / sp);
+            };
+            tiles = est(3) <= 1.05 * est(2) ? 3 : 2;
+        }
         int rpw = 0;
-        const int splits = mmqs_plan(N, K, di.cus, &rpw, bmt);
-        const size_t need = mmqs_need(M, K, N, di.cus, bmt);
+        const int splits = mmqs_plan(N, K, di.cus, &rpw, tiles);
+        const size_t need = mmqs_need(M, K, N, di.cus, tiles);
         std::unique_ptr<StreamScratch::Lease> lease;
         uint8_t* buf = fixed;
         if (fixed) {
@@ -1160,7 +1175,7 @@ int fq_fused_qkv(uint32_t dtype, const float* x, const void* wq, const void* wk,
         size_t need = 0;
         for (int i = 0; i < 3; ++i)
             if (ns[i] > 0)
-                for (int mt : {4, 2}) need = std::max(need, mmqs_need(M, K, ns[i], di.cus, mt));
+                for (int mt : {4, 3, 2}) need = std::max(need, mmqs_need(M, K, ns[i], di.cus, mt));
         StreamScratch::Lease l0(stream_scratch(dev, st, 0));
         uint8_t* p0 = nullptr;
         share = l0.get(need, st, &p0) == FQ_OK;
@@ -1249,7 +1264,7 @@ int fq_reserve_workspace(int M_max, int K_max, int N_max, void* stream) {
         for (int m = 2; m <= M_max; ++m) {
             need0 = std::max(need0, plan_mmq(m, K_max, n, di.cus).total);
             if (m <= 16 && Kp > 0)  // band kernel (from M = 2), four- and two-tile bands
-                for (int mt : {4, 2}) need0 = std::max(need0, mmqs_need(m, Kp, n, di.cus, mt));
+                for (int mt : {4, 3, 2}) need0 = std::max(need0, mmqs_need(m, Kp, n, di.cus, mt));
             if (m > 32 && Kp > 0) need0 = std::max(need0, plan_mmqp(m, Kp, n, di.cus, true).total);
             // the batch-1 kernel's K-split slabs for 2..4 tokens (at most 8)
             if (m <= 4) need0 = std::max(need0, (size_t)8 * m * n * sizeof(float));

@@ -617,6 +617,9 @@ const void* sfn_tw(int tw, bool bias) {
         case 2: return sfn<F, 2, WG>(bias);
     }
     // Q8_0, Q6_K: two tiles (LDS); Q3_K: two (four spill)
+    if constexpr (WG <= 512 && F == Q8_0) {
+        if (tw == 3) return sfn<F, 3, WG>(bias);
+    }
     if constexpr (WG <= 512 && F != Q8_0 && F != Q6_K && F != Q3_K) {
         switch (tw) {
             case 3: return sfn<F, 3, WG>(bias);
@@ -634,10 +637,11 @@ bool mmqs_supported(int dtype) {
 }
 
 // Tiles per work-group the kernel is instantiated for (bands of up to 16 TW
-// rows): Q8_0's 272-byte panels fit two per wave in LDS at 512 threads;
+// rows): Q8_0's 272-byte panels fit three per wave in LDS at 512 threads
+// (the host takes two or three);
 // Q6_K and Q3_K take two (their 16-element sub-blocks need twice the
 // operand registers per tile).
-int mmqs_max_tiles(int dtype) { return dtype == Q8_0 || dtype == Q6_K || dtype == Q3_K ? 2 : 4; }
+int mmqs_max_tiles(int dtype) { return dtype == Q8_0 ? 3 : dtype == Q6_K || dtype == Q3_K ? 2 : 4; }
 
 hipError_t launch_mmqs(int dtype, const MmqArgs& a, int rows_per_wg, int wg, int splits,
                        hipStream_t st) {
