@@ -397,12 +397,12 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
     // kernels further down take M = 4 0.4-0.7 us faster for Q4_0; Q8_0 only
     // while the bands number at most one per CU: lm_head 157 us on the
     // batch-1 kernel against 173), or, Q4_0 only, 3 from 16 MB with K of
-    // 14336 and more (3584 x 18944: 26.4 us on the batch-1 kernel).  Q4_0
-    // needs at most one band per CU or at least eight (18944 rows, 296 bands
-    // of 64, leave a second, mostly idle round: 28.6 against 24.8-27.6 us at
-    // M = 4..8; 152064 rows at M = 4..16 129-135 against 151-158 us); Q8_0
-    // takes any count (the fp16 MFMA path is slower at every one measured:
-    // 14336 x 4096 at M = 8 24.1 against 37.6 us)
+    // 14336 and more (3584 x 18944: 26.4 us on the batch-1 kernel).  At 3
+    // and 4 tokens Q4_0 needs at most one band per CU or at least eight
+    // (152064 rows at M = 4 129 against 151 us); from 5 tokens any count
+    // (18944 rows in three-tile bands, below: 24.5 against 27.5 us at M =
+    // 8).  Q8_0 takes any count (the fp16 MFMA path is slower at every one
+    // measured: 14336 x 4096 at M = 8 24.1 against 37.6 us)
     const int bmt = fq::mmqs_max_tiles((int)dtype);
     const long bands = ((long)N + 16 * bmt - 1) / (16 * bmt);
     // (Q4_1 as Q4_0)
@@ -412,7 +412,8 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
                           (M >= 5 ||
                            ((M == 4 ? q4x || bands <= di.cus : M == 3 && q4x && K >= 14336) &&
                             (int64_t)N * (K / g.be) * g.bb >= (16 << 20))) &&
-                          (dtype == FQ_DTYPE_Q8_0 || bands <= di.cus || bands >= 8L * di.cus);
+                          (dtype == FQ_DTYPE_Q8_0 || M >= 5 || bands <= di.cus ||
+                           bands >= 8L * di.cus);
     if (M >= 2 && M <= 4 && !blk_band && K > 0 && packable(dtype) &&
         (dtype == FQ_DTYPE_Q6_K || (int64_t)N * (K / g.be) * g.bb >= (8 << 20))) {
         // two to four tokens: the same kernel dots each weight unit it reads
@@ -481,7 +482,18 @@ int run_matmul(uint32_t dtype, const float* x, const void* w, const float* bias,
         // within 5 % (14336 x 4096 at M = 8: 24.2 us on two, 30.1 on three;
         // 152064 x 3584: 175.4 / 170.0; 18944 x 3584: 31.3 / 29.6)
         int tiles = bmt;
-        if (dtype == FQ_DTYPE_Q8_0) {
+        if (bmt == 4 && K / 256 < 32) {
+            // four-tile bands whose last round of work-groups is mostly idle
+            // (18944 rows: 296 bands on 256 CUs) take three tiles when those
+            // fill their rounds better (395 bands: Q4_0 at M = 8 27.5 ->
+            // 24.5 us, Q4_K at M = 16 31.3 -> 26.4, Q5_K 33.2 -> 27.7; at
+            // 14336 and 152064 rows four tiles measured faster)
+            auto fill = [&](int t) {
+                const long b = ((long)N + 16 * t - 1) / (16 * t);
+                return (double)b / (double)(((b + di.cus - 1) / di.cus) * di.cus);
+            };
+            if (N > 64L * di.cus && fill(4) < 0.6 && fill(3) > fill(4)) tiles = 3;
+        } else if (dtype == FQ_DTYPE_Q8_0) {
             auto est = [&](int mt) {
                 int r = 0;
                 const long sp = mmqs_plan(N, K, di.cus, &r, mt);
